@@ -1,0 +1,278 @@
+"""HiMuon optimizer-step benchmark on one MI355X.
+
+Metric: HiMuon step latency (ms) on one MI355X, with NS5
+TFLOP/s and its fraction of the bf16 dense MFMA peak.
+
+Default workload: the Qwen3-4B-shaped parameter set (36 layers x {q 4096x2560,
+k/v 1024x2560, o 2560x4096, gate/up 9728x2560, down 2560x9728}), bf16 params,
+fp32 grads ~N(0, 1e-3^2), tile_size=512 (13,860 tiles), the whole step
+captured in a hipGraph (LR/WD applied outside it, as the reference does).
+Inputs are synthetic and resident in HBM before the timed region.
+
+A "step" is one ``optimizer.step()``: graph replay (momentum + gather ->
+normaliser -> NS5 -> untile) plus the outside-graph WD/LR application.
+
+    python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline]
+
+Prints one JSON line. ``--gpus N`` with N > 1 exits: this build runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 4096 FLOP/clk x 2.4 GHz)
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    # name: (layers, [(h, w) per layer], tile_size, param dtype, description)
+    "qwen3-4b": (36, [(4096, 2560), (1024, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (9728, 2560), (2560, 9728)],
+                 512, torch.bfloat16, "Qwen3-4B-shaped param set (252 matrices), tile 512, hipGraph step"),
+    "qwen3-0.6b": (28, [(2048, 1024), (1024, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (3072, 1024), (1024, 3072)],
+                   512, torch.bfloat16, "Qwen3-0.6B-shaped param set (196 matrices), tile 512, hipGraph step"),
+    "qwen3-0.6b-full": (28, [(2048, 1024), (1024, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (3072, 1024), (1024, 3072)],
+                        1_000_000_000, torch.bfloat16, "Qwen3-0.6B-shaped set, full-matrix NS (Muon mode), hipGraph step"),
+    "llama3-8b-t128": (32, [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096), (14336, 4096), (4096, 14336)],
+                       128, torch.float32, "Llama-3-8B-shaped param set (224 matrices), tile 128, hipGraph step"),
+    "cfg1": (1, [(1024, 1024)], 256, torch.float32, "single 1024x1024 fp32 matrix, tile 256"),
+}
+
+
+def ns_flops(m: int, n: int) -> float:
+    """Algorithmic NS5 FLOPs of one m x n operand (m <= n): 5 (4 m^2 n + 2 m^3)."""
+    return 5.0 * (4.0 * m * m * n + 2.0 * m**3)
+
+
+def build_params(layers, shapes, dtype, seed=0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    params = []
+    for _ in range(layers):
+        for h, w in shapes:
+            p = torch.nn.Parameter(torch.empty(h, w, device="cuda", dtype=dtype))
+            p.data.normal_(0.0, 0.02, generator=g)
+            if dtype != torch.float32:
+                p.grad_dtype = torch.float32  # fp32 grads on bf16 params (the configs' setting)
+            p.grad = torch.empty(h, w, device="cuda", dtype=torch.float32)
+            p.grad.normal_(0.0, 1e-3, generator=g)
+            params.append(p)
+    return params
+
+
+def algorithmic_flops(opt) -> float:
+    total = 0.0
+    for grp in opt._groups:
+        t = grp["tiles"]
+        total += ns_flops(t.m, t.n) * t.n_tiles
+    return total
+
+
+def time_ns_stage(opt, reps: int) -> float:
+    """Average ms of the NS5 stage of one step (all chunks of all groups),
+    HIP events on the stream the kernels are launched on."""
+    s = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+
+    def run():
+        for g in opt._groups:
+            ofs = 0
+            for c in g["chunks"]:
+                g["tiles"].ns(ofs, c, g["steps"], opt._workspace, g["sub_batch"])
+                ofs += c
+
+    run()
+    torch.cuda.synchronize()
+    e0.record(s)
+    for _ in range(reps):
+        run()
+    e1.record(s)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def time_io_stage(opt, reps: int) -> tuple[float, float]:
+    """Average ms of gather (+normaliser) and of untile for one step."""
+    s = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    ev[0].record(s)
+    for _ in range(reps):
+        for g in opt._groups:
+            g["tiles"].gather()
+    ev[1].record(s)
+    for _ in range(reps):
+        for g in opt._groups:
+            g["tiles"].untile()
+    ev[2].record(s)
+    ev[2].synchronize()
+    return ev[0].elapsed_time(ev[1]) / reps, ev[1].elapsed_time(ev[2]) / reps
+
+
+def cpu_baseline(layers, shapes, tile, budget_s: float = 20.0):
+    """The CPU oracle (numpy, bf16-staged NS5) on a bounded sample of the same
+    workload: the matrices of one layer (or as many of its tiles as fit the time
+    budget), scaled to one full step. Returns the cpu_baseline JSON object."""
+    from oracle import himuon_oracle as O
+
+    threads = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    done_tiles = 0
+    total_tiles = 0
+    t_spent = 0.0
+    elems_done = 0
+    elems_total = 0
+    per_tile_times = []
+    for h, w in shapes:
+        th, tw = (tile, tile) if h * w > tile * tile else (h, w)
+        R, C = O.tile_grid(h, w, th, tw)
+        total_tiles += R * C * layers
+        elems_total += h * w * layers
+    t0 = time.perf_counter()
+    for h, w in shapes:
+        if time.perf_counter() - t0 > budget_s:
+            break
+        th, tw = (tile, tile) if h * w > tile * tile else (h, w)
+        g = (rng.standard_normal((h, w), dtype=np.float32) * 1e-3).astype(np.float32)
+        p = (rng.standard_normal((h, w), dtype=np.float32) * 0.02).astype(np.float32)
+        buf = np.zeros_like(g)
+        ts = time.perf_counter()
+        ge, buf = O.momentum(g, buf, 0.95, True)
+        tiles = O.tile(ge, th, tw)
+        # NS on as many tiles as the budget allows, one batch at a time
+        outs = []
+        k = 0
+        while k < tiles.shape[0] and time.perf_counter() - t0 < budget_s:
+            nb = min(8, tiles.shape[0] - k)
+            t1 = time.perf_counter()
+            outs.append(O.ns5_staged(tiles[k : k + nb]))
+            per_tile_times.append((time.perf_counter() - t1) / nb)
+            k += nb
+        done_tiles += k
+        if k == tiles.shape[0]:
+            u = O.untile(np.concatenate(outs), h, w)
+            p = O.apply_update(p, u * np.float32(O.lr_scale((th, tw))), 1e-2, 0.1, "bfloat16")
+            elems_done += h * w
+        t_spent += time.perf_counter() - ts
+    t_tile = float(np.mean(per_tile_times))
+    est_ms = t_tile * total_tiles * 1e3
+    return {
+        "value": round(est_ms, 1),
+        "unit": "ms/step (extrapolated)",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle/himuon_oracle.py numpy (OpenBLAS sgemm, bf16-staged NS5) on {done_tiles} of "
+                  f"{total_tiles} tiles ({t_spent:.1f} s); NS time per tile x all tiles; "
+                  f"cpu={platform.processor() or platform.machine()}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "this build runs the HiMuon step on one GPU only; "
+                                   "--gpus N > 1 is not supported (see DESIGN.md, sharding)"}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm device"}))
+        sys.exit(2)
+
+    from himuon_amd._native import load
+    from himuon_amd.optimizers.himuon import HiMuon
+
+    load()
+    layers, shapes, tile, pdtype, desc = CONFIGS[args.config]
+    params = build_params(layers, shapes, pdtype)
+    opt = HiMuon([{"params": params, "use_muon": True}], lr=1e-2, weight_decay=0.1, tile_size=tile,
+                 cuda_graph=True, cuda_graph_warmup=3)
+    warmup = max(args.warmup, 4)  # 3 eager steps + capture
+    for _ in range(warmup):
+        opt.step()
+    torch.cuda.synchronize()
+
+    s = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(s)
+    for _ in range(args.steps):
+        opt.step()
+    e1.record(s)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ev_ms = e0.elapsed_time(e1) / args.steps
+
+    ns_ms = time_ns_stage(opt, reps=max(3, args.steps // 2))
+    gather_ms, untile_ms = time_io_stage(opt, reps=max(3, args.steps // 2))
+    flops = algorithmic_flops(opt)
+    n_tiles = sum(g["tiles"].n_tiles for g in opt._groups)
+    n_el = sum(p.numel() for p in params)
+    ns_tflops = flops / (ns_ms * 1e-3) / 1e12
+
+    out = {
+        "metric": "HiMuon step latency (ms) on one MI355X; NS5 TFLOP/s and % of bf16 MFMA peak",
+        "value": round(wall_ms, 3),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall_ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": desc,
+            "config": args.config,
+            "matrices": len(params),
+            "elements": n_el,
+            "tiles": n_tiles,
+            "tile_size": tile,
+            "grad_dtype": "fp32",
+            "param_dtype": str(pdtype).replace("torch.", ""),
+        },
+        "step_ms_events": round(ev_ms, 3),
+        "ns5_ms": round(ns_ms, 3),
+        "ns5_tflops": round(ns_tflops, 1),
+        "ns5_frac_peak": round(ns_tflops / PEAK_BF16_TFLOPS, 4),
+        "gather_ms": round(gather_ms, 3),
+        "gather_gbs": round(14.0 * n_el / (gather_ms * 1e-3) / 1e9, 1),
+        "untile_ms": round(untile_ms, 3),
+        "untile_gbs": round(6.0 * n_el / (untile_ms * 1e-3) / 1e9, 1),
+        "roofline": {
+            "kernel": "ns5 stage (ns_gram_kernel x2 + ns_apply_kernel per iteration)",
+            "bound": "mfma",
+            "achieved": round(ns_tflops, 1),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(ns_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(layers, shapes, tile, args.cpu_budget)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,268 @@
+"""ctypes binding of libhimuon_hip.so (the C ABI declared in include/himuon_hip.h).
+
+Host-side plumbing only: pointers come from ``tensor.data_ptr()``, launches go
+to ``torch.cuda.current_stream()`` so they are recorded by ``torch.cuda.graph``
+capture. The library is required: every entry point raises ``RuntimeError`` if
+it is missing or the call fails (the reference raises the same way when its
+GPU kernels are unavailable, src/himuon/triton_kernels/__init__.py:8-19).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from ctypes import c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libhimuon_hip.so"
+
+ABI_VERSION = 1
+NS_ALIGN = 128
+DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+# Quintic coefficients and normaliser epsilon (himuon.py:237,242; ns5_smem.py:26-30).
+NS_A, NS_B, NS_C = 3.4445, -4.7750, 2.0315
+NS_EPS = 1e-7
+
+
+class ParamDesc(ctypes.Structure):
+    """Mirror of HimuonParamDesc (include/himuon_hip.h)."""
+
+    _fields_ = [
+        ("grad", c_void_p),
+        ("momentum", c_void_p),
+        ("update", c_void_p),
+        ("h", c_int64),
+        ("w", c_int64),
+        ("ld_grad", c_int64),
+        ("ld_mom", c_int64),
+        ("ld_upd", c_int64),
+        ("tile0", c_int64),
+        ("R", c_int32),
+        ("C", c_int32),
+        ("upd_scale", c_float),
+        ("mu", c_float),
+        ("nesterov", c_int32),
+        ("reserved", c_int32),
+    ]
+
+
+assert ctypes.sizeof(ParamDesc) == 96
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "himuon_abi_version": (c_int, []),
+    "himuon_error_string": (ctypes.c_char_p, [c_int]),
+    "himuon_gather_partials_per_tile": (c_int, [c_int, c_int, c_int, c_int]),
+    "himuon_momentum_gather": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p],
+    ),
+    "himuon_tile_scale": (c_int, [c_void_p, c_int, c_int64, c_float, c_void_p, c_void_p]),
+    "himuon_ns5_workspace_bytes": (c_size_t, [c_int64, c_int, c_int]),
+    "himuon_ns5": (
+        c_int,
+        [
+            c_void_p,
+            c_void_p,
+            c_void_p,
+            c_int64,
+            c_int,
+            c_int,
+            c_int,
+            c_float,
+            c_float,
+            c_float,
+            c_void_p,
+            c_size_t,
+            c_int64,
+            c_void_p,
+        ],
+    ),
+    "himuon_untile": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p],
+    ),
+}
+
+_lib = None
+
+
+def lib_path() -> Path:
+    return Path(os.environ.get("HIMUON_LIB", str(LIB_PATH)))
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once; raise RuntimeError if it is missing or stale."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = lib_path()
+    if not path.exists():
+        raise RuntimeError(
+            f"libhimuon_hip.so not found at {path}. Build it with `python -m himuon_amd.build` "
+            "(hipcc --offload-arch=gfx950). HiMuon has no CPU fallback."
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    ver = lib.himuon_abi_version()
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"libhimuon_hip.so ABI {ver} != expected {ABI_VERSION}; rebuild it")
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().himuon_error_string(rc).decode()
+        raise RuntimeError(f"{what} failed: {msg} (code {rc})")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"HiMuon HIP path supports float32/bfloat16/float16 grads, got {dtype}")
+
+
+# ---------------------------------------------------------------------------
+# Geometry
+# ---------------------------------------------------------------------------
+def round_up(x: int, a: int) -> int:
+    return (x + a - 1) // a * a
+
+
+def ns_geometry(tile_h: int, tile_w: int) -> tuple[int, int, int, int, bool]:
+    """(m, n, mp, np, transposed) of the NS operand for a tile_h x tile_w tile:
+    NS runs on the tile's transpose when it is tall (himuon.py:240-241,276-278)."""
+    trans = tile_h > tile_w
+    m, n = (tile_w, tile_h) if trans else (tile_h, tile_w)
+    return m, n, round_up(m, NS_ALIGN), round_up(n, NS_ALIGN), trans
+
+
+def gather_partials_per_tile(tile_h: int, tile_w: int, mp: int, np_: int) -> int:
+    n = load().himuon_gather_partials_per_tile(tile_h, tile_w, mp, np_)
+    _check(0 if n > 0 else n, "himuon_gather_partials_per_tile")
+    return n
+
+
+def ns5_workspace_bytes(sub_batch: int, mp: int, np_: int) -> int:
+    return int(load().himuon_ns5_workspace_bytes(sub_batch, mp, np_))
+
+
+def default_sub_batch(n_tiles: int, mp: int, np_: int) -> int:
+    """Tiles per NS sub-batch: about 64 MiB of bf16 NS operand per launch, so
+    a sub-batch's X/A/B intermediates stay within MI355X's 256 MB MALL."""
+    env = os.environ.get("HIMUON_NS_SUB_BATCH")
+    if env:
+        return max(1, min(n_tiles, int(env)))
+    target = 64 << 20
+    return max(1, min(n_tiles, target // (mp * np_ * 2)))
+
+
+# ---------------------------------------------------------------------------
+# Descriptor tables
+# ---------------------------------------------------------------------------
+def make_desc_table(descs: list[ParamDesc], device) -> torch.Tensor:
+    """Copy an array of ParamDesc to device memory (uint8 tensor)."""
+    arr = (ParamDesc * len(descs))(*descs)
+    host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
+    return host.to(device)
+
+
+# ---------------------------------------------------------------------------
+# Entry points
+# ---------------------------------------------------------------------------
+def momentum_gather(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtype, tiles, partials):
+    _check(
+        load().himuon_momentum_gather(
+            desc_table.data_ptr(),
+            n_params,
+            n_tiles,
+            tile_h,
+            tile_w,
+            mp,
+            np_,
+            dtype_code(dtype),
+            tiles.data_ptr(),
+            partials.data_ptr(),
+            _stream(),
+        ),
+        "himuon_momentum_gather",
+    )
+
+
+def tile_scale(partials, per_tile, n_tiles, inv, eps=NS_EPS):
+    _check(
+        load().himuon_tile_scale(partials.data_ptr(), per_tile, n_tiles, eps, inv.data_ptr(), _stream()),
+        "himuon_tile_scale",
+    )
+
+
+def ns5(tiles_in, tiles_out, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, NS_B, NS_C)):
+    a, b, c = coeffs
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(
+        load().himuon_ns5(
+            tiles_in.data_ptr(),
+            tiles_out.data_ptr(),
+            inv.data_ptr(),
+            n_tiles,
+            mp,
+            np_,
+            steps,
+            a,
+            b,
+            c,
+            ws_ptr,
+            ws_bytes,
+            sub_batch,
+            _stream(),
+        ),
+        "himuon_ns5",
+    )
+
+
+def untile(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtype, tiles):
+    _check(
+        load().himuon_untile(
+            desc_table.data_ptr(),
+            n_params,
+            n_tiles,
+            tile_h,
+            tile_w,
+            mp,
+            np_,
+            dtype_code(dtype),
+            tiles.data_ptr(),
+            _stream(),
+        ),
+        "himuon_untile",
+    )
+
+
+def lr_scale(block_shape, lr_adjust: str = "tile") -> float:
+    """adjust_lr_for_muon(1.0, block) (himuon.py:181-186)."""
+    if lr_adjust == "none":
+        return 1.0
+    a, b = block_shape[:2]
+    return 0.2 * math.sqrt(max(a, b))

@@ -1,0 +1,124 @@
+// Shared device helpers for the HiMuon gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/himuon_hip.h"
+
+#define HM_DEV __device__ __forceinline__
+
+// ---------------------------------------------------------------------------
+// bf16 / fp16 <-> fp32. Rounding is round-to-nearest-even with quiet NaNs,
+// the rounding torch's `.to(torch.bfloat16)` performs.
+// ---------------------------------------------------------------------------
+HM_DEV float bf16_to_f32(uint32_t v) { return __uint_as_float(v << 16); }
+
+HM_DEV uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // canonical quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Round an fp32 value to the nearest bf16 and return it as fp32.
+HM_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+HM_DEV float f16_to_f32(uint16_t v) {
+  _Float16 h;
+  __builtin_memcpy(&h, &v, 2);
+  return (float)h;
+}
+
+HM_DEV uint16_t f32_to_f16(float f) {
+  _Float16 h = (_Float16)f;
+  uint16_t v;
+  __builtin_memcpy(&v, &h, 2);
+  return v;
+}
+
+// Load / store one element of a gradient-typed tensor as fp32.
+template <int DT>
+HM_DEV float load_elem(const void* p, int64_t i) {
+  if constexpr (DT == HIMUON_DTYPE_F32) {
+    return static_cast<const float*>(p)[i];
+  } else if constexpr (DT == HIMUON_DTYPE_BF16) {
+    return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  } else {
+    return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  }
+}
+
+template <int DT>
+HM_DEV float round_to(float f) {
+  if constexpr (DT == HIMUON_DTYPE_F32) {
+    return f;
+  } else if constexpr (DT == HIMUON_DTYPE_BF16) {
+    return round_bf16(f);
+  } else {
+    return f16_to_f32(f32_to_f16(f));
+  }
+}
+
+template <int DT>
+HM_DEV void store_elem(void* p, int64_t i, float v) {
+  if constexpr (DT == HIMUON_DTYPE_F32) {
+    static_cast<float*>(p)[i] = v;
+  } else if constexpr (DT == HIMUON_DTYPE_BF16) {
+    static_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_bf16(v);
+  } else {
+    static_cast<uint16_t*>(p)[i] = f32_to_f16(v);
+  }
+}
+
+// Pack two bf16 bit patterns (lo, hi) into one dword.
+HM_DEV uint32_t pack2(uint32_t lo, uint32_t hi) { return (lo & 0xffffu) | (hi << 16); }
+
+// ---------------------------------------------------------------------------
+// Work-item -> XCD mapping. MI355X dispatches consecutive workgroups
+// round-robin over its 8 XCDs, each with a private L2. Items that share data
+// (the blocks of one NS tile) are given consecutive item numbers; this maps
+// workgroup b to item (b % 8) * per_xcd + b / 8 so that each XCD walks one
+// contiguous range of items and a tile's blocks share an L2.
+// Grid size must be 8 * per_xcd, per_xcd = ceil(total / 8).
+// ---------------------------------------------------------------------------
+constexpr int kNumXcd = 8;
+
+HM_DEV int64_t xcd_item(int64_t total) {
+  const int64_t per_xcd = (total + kNumXcd - 1) / kNumXcd;
+  return (int64_t)(blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
+}
+
+inline int64_t xcd_grid(int64_t total) {
+  const int64_t per_xcd = (total + kNumXcd - 1) / kNumXcd;
+  return per_xcd * kNumXcd;
+}
+
+// Find the parameter owning tile t: the last p with params[p].tile0 <= t.
+HM_DEV int find_param(const HimuonParamDesc* __restrict__ params, int n_params, int64_t t) {
+  int lo = 0, hi = n_params - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (params[mid].tile0 <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Wave/block reduction of a float (deterministic order).
+HM_DEV float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <int NT>
+HM_DEV float block_sum(float v, float* red /* >= NT/64 floats of LDS */) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+  if (threadIdx.x == 0) {
+    for (int i = 0; i < NT / 64; ++i) s += red[i];
+  }
+  return s;  // valid in thread 0 only
+}

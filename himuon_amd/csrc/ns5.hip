@@ -1,0 +1,369 @@
+// Batched quintic Newton-Schulz (NS5) on gfx950 bf16 MFMA, fp32 accumulation.
+//
+// Per NS tile (m x n, m <= n, zero padded to mp x np) and per iteration:
+//   A = bf16(X X^T)                      -> ns_gram_kernel (alpha=1, beta=0)
+//   B = bf16(c A A^T + b A)              -> ns_gram_kernel (alpha=c, beta=b)
+//   X = bf16(bf16(B X) + a X)            -> ns_apply_kernel
+// following the rounding points of the reference kernels
+// (triton_kernels/XXT.py:55-75, ba_plus_cAA.py:58-85, fused_bmm_add.py:65-88,
+// ns5_smem.py:84-101). A and B are symmetric: the gram kernel computes only
+// the lower-triangular 128x128 blocks and stores each block twice (as itself
+// and mirrored), so both products cost half the dense FLOPs.
+//
+// Iteration 0 reads the raw bf16 tile and applies the per-tile Frobenius
+// normaliser while staging operands into LDS: X0 = bf16(x * inv[t])
+// (himuon.py:242, ns5_smem.py:84-87).
+//
+// Block tile 128x128x64, 256 threads = 4 waves in a 2x2 grid, each wave owns a
+// 64x64 sub-block = 2x2 MFMA 32x32x16 tiles. Operands are double buffered in
+// LDS with register prefetch of the next K slab. Blocks are mapped to XCDs so
+// all blocks of one NS tile share an L2.
+#include <algorithm>
+
+#include "common.h"
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int kLd = BK + 8;  // padded LDS row pitch (elements) of k-contiguous operands
+
+HM_DEV f32x16_t mfma_32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// x -> bf16(x * s) for 8 packed bf16 values.
+HM_DEV u32x4_t scale8(u32x4_t v, float s) {
+  u32x4_t o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float lo = bf16_to_f32(v[k] & 0xffffu) * s;
+    const float hi = __uint_as_float(v[k] & 0xffff0000u) * s;
+    o[k] = pack2(f32_to_bf16(lo), f32_to_bf16(hi));
+  }
+  return o;
+}
+
+HM_DEV uint32_t half16(uint32_t w, int h) { return h ? (w >> 16) : (w & 0xffffu); }
+
+// ---------------------------------------------------------------------------
+// C = bf16(alpha * S S^T + beta * S) for each tile; S is M x K (row pitch ldS),
+// C is M x M (row pitch ldC). Only blocks bi >= bj are computed; every block
+// is written at (bi, bj) and mirrored at (bj, bi), so C is exactly symmetric.
+// beta != 0 requires K == M (S square).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads, 2) void ns_gram_kernel(
+    const uint16_t* __restrict__ S, int64_t s_bs, int ldS, uint16_t* __restrict__ C,
+    int64_t c_bs, int ldC, const float* __restrict__ inv, int M, int K, int64_t ntiles,
+    float alpha, float beta) {
+  __shared__ __attribute__((aligned(16))) uint16_t sI[2][BM * kLd];
+  __shared__ __attribute__((aligned(16))) uint16_t sJ[2][BN * kLd];
+
+  const int nb = M / BM;
+  const int npairs = nb * (nb + 1) / 2;
+  const int64_t total = ntiles * npairs;
+  const int64_t item = xcd_item(total);
+  if (item >= total) return;
+  const int64_t tile = item / npairs;
+  const int p = (int)(item % npairs);
+  int bi = 0;
+  while ((bi + 1) * (bi + 2) / 2 <= p) ++bi;
+  const int bj = p - bi * (bi + 1) / 2;
+
+  const uint16_t* St = S + tile * s_bs;
+  const uint16_t* Si = St + (int64_t)bi * BM * ldS;
+  const uint16_t* Sj = St + (int64_t)bj * BN * ldS;
+  const bool scaled = inv != nullptr;
+  const float sc = scaled ? inv[tile] : 1.f;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lrow = tid >> 3, lkv = (tid & 7) * 8;  // loader: rows lrow + 32q, k offset lkv
+
+  u32x4_t ra[4], rb[4];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = lrow + 32 * q;
+      ra[q] = *reinterpret_cast<const u32x4_t*>(Si + (int64_t)row * ldS + k0 + lkv);
+      rb[q] = *reinterpret_cast<const u32x4_t*>(Sj + (int64_t)row * ldS + k0 + lkv);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = lrow + 32 * q;
+      u32x4_t a = ra[q], b = rb[q];
+      if (scaled) {
+        a = scale8(a, sc);
+        b = scale8(b, sc);
+      }
+      *reinterpret_cast<u32x4_t*>(&sI[buf][row * kLd + lkv]) = a;
+      *reinterpret_cast<u32x4_t*>(&sJ[buf][row * kLd + lkv]) = b;
+    }
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
+
+  const int nk = K / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int kk = ks * 16 + (lane >> 5) * 8;
+      u32x4_t a[2], b[2];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+        a[mi] = *reinterpret_cast<const u32x4_t*>(
+            &sI[cur][(wm * 64 + mi * 32 + (lane & 31)) * kLd + kk]);
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+        b[ni] = *reinterpret_cast<const u32x4_t*>(
+            &sJ[cur][(wn * 64 + ni * 32 + (lane & 31)) * kLd + kk]);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma_32x32x16(a[mi], b[ni], acc[mi][ni]);
+    }
+    if (kt + 1 < nk) lstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue. MFMA 32x32 output layout: register r of lane l holds
+  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+  uint16_t* Ct = C + tile * c_bs;
+  const bool offdiag = bi > bj;
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = bi * BM + wm * 64 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int j = bj * BN + wn * 64 + ni * 32 + (lane & 31);
+        float v = alpha * acc[mi][ni][r];
+        if (beta != 0.f) {
+          float s = bf16_to_f32(St[(int64_t)i * ldS + j]);
+          if (scaled) s = round_bf16(s * sc);
+          v = fmaf(beta, s, v);
+        }
+        const uint16_t h = (uint16_t)f32_to_bf16(v);
+        if (offdiag || i >= j) Ct[(int64_t)i * ldC + j] = h;
+        if (offdiag || i > j) Ct[(int64_t)j * ldC + i] = h;
+      }
+}
+
+// ---------------------------------------------------------------------------
+// Y = bf16(bf16(Bm X) + a X) for each tile; Bm is M x M symmetric (pitch M),
+// X and Y are M x N (pitch N). X is the MFMA B operand with the contraction
+// along its rows, so each 4x8 register block of X is transposed into a
+// k-octet-major LDS layout sX[k/8][j][k%8] that serves 16-byte operand reads.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads, 2) void ns_apply_kernel(
+    const uint16_t* __restrict__ Bm, int64_t b_bs, const uint16_t* __restrict__ X, int64_t x_bs,
+    uint16_t* __restrict__ Y, int64_t y_bs, const float* __restrict__ inv, int M, int N,
+    int64_t ntiles, float a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * kLd];
+  __shared__ __attribute__((aligned(16))) uint16_t sX[2][(BK / 8) * BN * 8];
+
+  const int nbi = M / BM, nbj = N / BN;
+  const int blocks = nbi * nbj;
+  const int64_t total = ntiles * blocks;
+  const int64_t item = xcd_item(total);
+  if (item >= total) return;
+  const int64_t tile = item / blocks;
+  const int blk = (int)(item % blocks);
+  const int bi = blk / nbj, bj = blk % nbj;
+
+  const uint16_t* Ai = Bm + tile * b_bs + (int64_t)bi * BM * M;
+  const uint16_t* Xt = X + tile * x_bs;
+  const bool scaled = inv != nullptr;
+  const float sc = scaled ? inv[tile] : 1.f;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lrow = tid >> 3, lkv = (tid & 7) * 8;    // Bm loader
+  const int xkq = tid >> 4, xjo = (tid & 15) * 8;    // X loader: rows 4*xkq..+3, cols xjo..+7
+
+  u32x4_t ra[4], rx[4];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = lrow + 32 * q;
+      ra[q] = *reinterpret_cast<const u32x4_t*>(Ai + (int64_t)row * M + k0 + lkv);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+      rx[rr] = *reinterpret_cast<const u32x4_t*>(Xt + (int64_t)(k0 + 4 * xkq + rr) * N +
+                                                 bj * BN + xjo);
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = lrow + 32 * q;
+      *reinterpret_cast<u32x4_t*>(&sA[buf][row * kLd + lkv]) = ra[q];
+    }
+    u32x4_t x[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) x[rr] = scaled ? scale8(rx[rr], sc) : rx[rr];
+    uint16_t* base = &sX[buf][(xkq >> 1) * BN * 8 + (xkq & 1) * 4];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int w = e >> 1, h = e & 1;
+      u32x2_t d;
+      d[0] = pack2(half16(x[0][w], h), half16(x[1][w], h));
+      d[1] = pack2(half16(x[2][w], h), half16(x[3][w], h));
+      *reinterpret_cast<u32x2_t*>(base + (xjo + e) * 8) = d;
+    }
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
+
+  const int nk = M / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int kk = ks * 16 + (lane >> 5) * 8;
+      const int koct = ks * 2 + (lane >> 5);
+      u32x4_t av[2], bv[2];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+        av[mi] = *reinterpret_cast<const u32x4_t*>(
+            &sA[cur][(wm * 64 + mi * 32 + (lane & 31)) * kLd + kk]);
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+        bv[ni] = *reinterpret_cast<const u32x4_t*>(
+            &sX[cur][(koct * BN + wn * 64 + ni * 32 + (lane & 31)) * 8]);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma_32x32x16(av[mi], bv[ni], acc[mi][ni]);
+    }
+    if (kt + 1 < nk) lstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  uint16_t* Yt = Y + tile * y_bs;
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = bi * BM + wm * 64 + mi * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int j = bj * BN + wn * 64 + ni * 32 + (lane & 31);
+        float xv = bf16_to_f32(Xt[(int64_t)i * N + j]);
+        if (scaled) xv = round_bf16(xv * sc);
+        const float bx = round_bf16(acc[mi][ni][r]);
+        Yt[(int64_t)i * N + j] = (uint16_t)f32_to_bf16(fmaf(a, xv, bx));
+      }
+}
+
+// Y = bf16(X * inv[t]) (steps == 0) or a plain copy (inv == nullptr).
+__global__ __launch_bounds__(kThreads) void ns_scale_copy_kernel(const uint16_t* __restrict__ X,
+                                                                uint16_t* __restrict__ Y,
+                                                                const float* __restrict__ inv,
+                                                                int64_t per_tile, int64_t ntiles) {
+  const int64_t nvec = ntiles * per_tile / 8;
+  for (int64_t v = (int64_t)blockIdx.x * kThreads + threadIdx.x; v < nvec;
+       v += (int64_t)gridDim.x * kThreads) {
+    u32x4_t q = reinterpret_cast<const u32x4_t*>(X)[v];
+    if (inv) q = scale8(q, inv[(v * 8) / per_tile]);
+    reinterpret_cast<u32x4_t*>(Y)[v] = q;
+  }
+}
+
+}  // namespace
+
+extern "C" size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np) {
+  if (sub_batch <= 0 || mp <= 0 || np <= 0) return 0;
+  const size_t sq = (size_t)sub_batch * mp * mp * sizeof(uint16_t);
+  const size_t rect = (size_t)sub_batch * mp * np * sizeof(uint16_t);
+  return 2 * sq + 2 * rect;
+}
+
+extern "C" int himuon_ns5(const uint16_t* tiles_in, uint16_t* tiles_out, const float* inv,
+                          int64_t n_tiles, int mp, int np, int steps, float a, float b, float c,
+                          void* workspace, size_t workspace_bytes, int64_t sub_batch,
+                          void* stream) {
+  if (!tiles_in || !tiles_out || !inv || n_tiles < 0 || steps < 0 || mp <= 0 || np <= 0 ||
+      mp > np || mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN || sub_batch <= 0)
+    return HIMUON_EINVAL;
+  if (n_tiles == 0) return 0;
+  const int64_t sb = sub_batch < n_tiles ? sub_batch : n_tiles;
+  if (steps > 0 && (!workspace || workspace_bytes < himuon_ns5_workspace_bytes(sb, mp, np)))
+    return HIMUON_ENOSPC;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t sq = (int64_t)mp * mp, rect = (int64_t)mp * np;
+
+  if (steps == 0) {
+    const int64_t nvec = n_tiles * rect / 8;
+    const unsigned grid = (unsigned)std::min<int64_t>((nvec + kThreads - 1) / kThreads, 65536);
+    hipLaunchKernelGGL(ns_scale_copy_kernel, dim3(grid), dim3(kThreads), 0, s, tiles_in,
+                       tiles_out, inv, rect, n_tiles);
+    return (int)hipGetLastError();
+  }
+
+  uint16_t* wsA = static_cast<uint16_t*>(workspace);
+  uint16_t* wsB = wsA + sb * sq;
+  uint16_t* wsX[2] = {wsB + sb * sq, wsB + sb * sq + sb * rect};
+  const int nb = mp / BM;
+  const int npairs = nb * (nb + 1) / 2;
+  const int apply_blocks = (mp / BM) * (np / BN);
+
+  for (int64_t s0 = 0; s0 < n_tiles; s0 += sb) {
+    const int64_t cnt = std::min<int64_t>(sb, n_tiles - s0);
+    const uint16_t* cur = tiles_in + s0 * rect;
+    uint16_t* out = tiles_out + s0 * rect;
+    const float* cur_inv = inv + s0;
+    const bool copy_back = (steps == 1 && cur == out);
+    for (int it = 0; it < steps; ++it) {
+      hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(cnt * npairs)), dim3(kThreads), 0,
+                         s, cur, rect, np, wsA, sq, mp, cur_inv, mp, np, cnt, 1.0f, 0.0f);
+      hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(cnt * npairs)), dim3(kThreads), 0,
+                         s, wsA, sq, mp, wsB, sq, mp, nullptr, mp, mp, cnt, c, b);
+      uint16_t* dst = (it == steps - 1 && !copy_back) ? out : wsX[it & 1];
+      hipLaunchKernelGGL(ns_apply_kernel, dim3((unsigned)xcd_grid(cnt * apply_blocks)),
+                         dim3(kThreads), 0, s, wsB, sq, cur, rect, dst, rect, cur_inv, mp, np, cnt,
+                         a);
+      cur = dst;
+      cur_inv = nullptr;
+    }
+    if (copy_back) {
+      const int64_t nvec = cnt * rect / 8;
+      const unsigned grid = (unsigned)std::min<int64_t>((nvec + kThreads - 1) / kThreads, 65536);
+      hipLaunchKernelGGL(ns_scale_copy_kernel, dim3(grid), dim3(kThreads), 0, s, cur, out,
+                         nullptr, rect, cnt);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
+  return 0;
+}

@@ -1,0 +1,432 @@
+// Memory-bound kernels around the Newton-Schulz core:
+//   * momentum_gather: Nesterov momentum + zero-padded tile gather into the
+//     bf16 NS tile buffer + per-slab sum of squares (himuon.py:350-357,
+//     704-719, 239-242).
+//   * tile_scale: per-tile 1 / (||X||_F + eps) (himuon.py:242).
+//   * untile: NS tile buffer -> per-parameter update (himuon.py:315-329).
+// All are HBM-bound: each element is read/written once (14 B/el for fp32
+// gather, 6 B/el for fp32 untile), with 16-byte accesses on both sides.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kSlabRows = 32;  // NS rows per gather/untile work item (plain tiles)
+constexpr int kBlk = 64;       // NS block edge for the transposed variants
+constexpr int kBlkPitch = kBlk + 8;
+
+struct Geo {
+  int tile_h, tile_w, mp, np;
+};
+
+// 8 consecutive elements of a gradient-typed row, as fp32.
+template <int DT>
+HM_DEV void load8(const void* base, int64_t off, float v[8]) {
+  if constexpr (DT == HIMUON_DTYPE_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+    const float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (DT == HIMUON_DTYPE_BF16) {
+        v[2 * k] = bf16_to_f32(w[k] & 0xffffu);
+        v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+      } else {
+        v[2 * k] = f16_to_f32((uint16_t)(w[k] & 0xffffu));
+        v[2 * k + 1] = f16_to_f32((uint16_t)(w[k] >> 16));
+      }
+    }
+  }
+}
+
+template <int DT>
+HM_DEV void store8(void* base, int64_t off, const float v[8]) {
+  if constexpr (DT == HIMUON_DTYPE_F32) {
+    float4* p = reinterpret_cast<float4*>(static_cast<float*>(base) + off);
+    p[0] = make_float4(v[0], v[1], v[2], v[3]);
+    p[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (DT == HIMUON_DTYPE_BF16) {
+        w[k] = pack2(f32_to_bf16(v[2 * k]), f32_to_bf16(v[2 * k + 1]));
+      } else {
+        w[k] = pack2(f32_to_f16(v[2 * k]), f32_to_f16(v[2 * k + 1]));
+      }
+    }
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + off) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <int DT>
+HM_DEV bool aligned16(const void* base, int64_t off) {
+  constexpr int es = (DT == HIMUON_DTYPE_F32) ? 4 : 2;
+  return ((reinterpret_cast<uintptr_t>(base) + (uintptr_t)off * es) & 15u) == 0;
+}
+
+// Momentum for one element (himuon.py:354-356); returns the NS input and
+// writes the new momentum value to *m. Results are rounded to the tensor
+// dtype where torch stores them: buf.mul_(mu) and .add_(g) each store (two
+// roundings, no contraction); g.add(buf, alpha=mu) is one fp32 fused
+// multiply-add stored once, as torch evaluates `self + alpha * other`.
+template <int DT>
+HM_DEV float momentum_elem(float g, float* m, float mu, bool nesterov, bool has_mom) {
+  // (__fmul_rn/__fadd_rn would still be contracted into an FMA; plain
+  // operators under contract(off) are not.)
+#pragma clang fp contract(off)
+  if (!has_mom) return g;
+  const float prod = round_to<DT>(mu * *m);
+  const float mb = round_to<DT>(prod + g);
+  *m = mb;
+  if (!nesterov) return mb;
+  float e = __builtin_fmaf(mu, mb, g);
+  // Keep the fp32 rounding of the fma before the fp16 cast (the compiler
+  // would otherwise emit one fma with a direct fp16 result).
+  if constexpr (DT == HIMUON_DTYPE_F16) asm volatile("" : "+v"(e));
+  return round_to<DT>(e);
+}
+
+// ---------------------------------------------------------------------------
+// Gather, plain tiles (tile_h <= tile_w): NS (i, j) = tile (i, j).
+// Work item = (tile, slab of kSlabRows NS rows).
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(kThreads) void gather_plain_kernel(
+    const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
+    uint16_t* __restrict__ tiles, float* __restrict__ partials) {
+  __shared__ float red[kThreads / 64];
+  const int slabs = geo.mp / kSlabRows;
+  const int64_t item = xcd_item(n_tiles * slabs);
+  if (item >= n_tiles * slabs) return;
+  const int64_t t = item / slabs;
+  const int q = (int)(item % slabs);
+  const HimuonParamDesc& P = params[find_param(params, n_params, t)];
+  const int64_t lt = t - P.tile0;
+  const int r = (int)(lt / P.C), c = (int)(lt % P.C);
+  const bool has_mom = P.momentum != nullptr;
+  const float mu = P.mu;
+  const bool nesterov = P.nesterov != 0;
+  const int vpr = geo.np / 8;  // 8-element vectors per NS row
+  uint16_t* out = tiles + t * (int64_t)geo.mp * geo.np;
+  float ssq = 0.f;
+  for (int v = threadIdx.x; v < kSlabRows * vpr; v += kThreads) {
+    const int i = q * kSlabRows + v / vpr;
+    const int j0 = (v % vpr) * 8;
+    const int64_t pr = (int64_t)r * geo.tile_h + i;
+    const int64_t pc = (int64_t)c * geo.tile_w + j0;
+    float x[8];
+    const bool row_ok = i < geo.tile_h && pr < P.h;
+    const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
+    const bool fast = row_ok && j0 + 8 <= geo.tile_w && pc + 8 <= P.w &&
+                      aligned16<DT>(P.grad, og) && (!has_mom || aligned16<DT>(P.momentum, om));
+    if (fast) {
+      float g[8], m[8];
+      load8<DT>(P.grad, og, g);
+      if (has_mom) load8<DT>(P.momentum, om, m);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = momentum_elem<DT>(g[e], &m[e], mu, nesterov, has_mom);
+      if (has_mom) store8<DT>(P.momentum, om, m);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = 0.f;
+        if (row_ok && j0 + e < geo.tile_w && pc + e < P.w) {
+          const float g = load_elem<DT>(P.grad, og + e);
+          float m = has_mom ? load_elem<DT>(P.momentum, om + e) : 0.f;
+          x[e] = momentum_elem<DT>(g, &m, mu, nesterov, has_mom);
+          if (has_mom) store_elem<DT>(P.momentum, om + e, m);
+        }
+      }
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = f32_to_bf16(x[2 * k]), hi = f32_to_bf16(x[2 * k + 1]);
+      const float flo = bf16_to_f32(lo), fhi = bf16_to_f32(hi);
+      ssq = fmaf(flo, flo, ssq);
+      ssq = fmaf(fhi, fhi, ssq);
+      w[k] = pack2(lo, hi);
+    }
+    *reinterpret_cast<uint4*>(out + (int64_t)i * geo.np + j0) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  const float s = block_sum<kThreads>(ssq, red);
+  if (threadIdx.x == 0) partials[t * slabs + q] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Gather, transposed tiles (tile_h > tile_w): NS (i, j) = tile (j, i).
+// Work item = (tile, 64x64 NS block); the block is transposed through LDS so
+// both the parameter reads and the NS writes are 16-byte row accesses.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(kThreads) void gather_trans_kernel(
+    const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
+    uint16_t* __restrict__ tiles, float* __restrict__ partials) {
+  __shared__ uint16_t sT[kBlk * kBlkPitch];  // [NS row i][NS col j]
+  __shared__ float red[kThreads / 64];
+  const int bi_n = geo.mp / kBlk, bj_n = geo.np / kBlk;
+  const int blocks = bi_n * bj_n;
+  const int64_t item = xcd_item(n_tiles * blocks);
+  if (item >= n_tiles * blocks) return;
+  const int64_t t = item / blocks;
+  const int b = (int)(item % blocks);
+  const int i0 = (b / bj_n) * kBlk, j0 = (b % bj_n) * kBlk;
+  const HimuonParamDesc& P = params[find_param(params, n_params, t)];
+  const int64_t lt = t - P.tile0;
+  const int r = (int)(lt / P.C), c = (int)(lt % P.C);
+  const bool has_mom = P.momentum != nullptr;
+  const float mu = P.mu;
+  const bool nesterov = P.nesterov != 0;
+  float ssq = 0.f;
+  // Load: tile-local row tr = j0 + rr, cols tc = i0 + 8*cv .. +7.
+  for (int v = threadIdx.x; v < kBlk * (kBlk / 8); v += kThreads) {
+    const int rr = v / (kBlk / 8), cv = v % (kBlk / 8);
+    const int tr = j0 + rr, tc = i0 + cv * 8;
+    const int64_t pr = (int64_t)r * geo.tile_h + tr;
+    const int64_t pc = (int64_t)c * geo.tile_w + tc;
+    const bool row_ok = tr < geo.tile_h && pr < P.h;
+    const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
+    float x[8];
+    const bool fast = row_ok && tc + 8 <= geo.tile_w && pc + 8 <= P.w &&
+                      aligned16<DT>(P.grad, og) && (!has_mom || aligned16<DT>(P.momentum, om));
+    if (fast) {
+      float g[8], m[8];
+      load8<DT>(P.grad, og, g);
+      if (has_mom) load8<DT>(P.momentum, om, m);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = momentum_elem<DT>(g[e], &m[e], mu, nesterov, has_mom);
+      if (has_mom) store8<DT>(P.momentum, om, m);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = 0.f;
+        if (row_ok && tc + e < geo.tile_w && pc + e < P.w) {
+          const float g = load_elem<DT>(P.grad, og + e);
+          float m = has_mom ? load_elem<DT>(P.momentum, om + e) : 0.f;
+          x[e] = momentum_elem<DT>(g, &m, mu, nesterov, has_mom);
+          if (has_mom) store_elem<DT>(P.momentum, om + e, m);
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t h = f32_to_bf16(x[e]);
+      const float f = bf16_to_f32(h);
+      ssq = fmaf(f, f, ssq);
+      sT[(cv * 8 + e) * kBlkPitch + rr] = (uint16_t)h;
+    }
+  }
+  __syncthreads();
+  uint16_t* out = tiles + t * (int64_t)geo.mp * geo.np;
+  for (int v = threadIdx.x; v < kBlk * (kBlk / 8); v += kThreads) {
+    const int ii = v / (kBlk / 8), jv = v % (kBlk / 8);
+    const uint4 q = *reinterpret_cast<const uint4*>(&sT[ii * kBlkPitch + jv * 8]);
+    *reinterpret_cast<uint4*>(out + (int64_t)(i0 + ii) * geo.np + j0 + jv * 8) = q;
+  }
+  const float s = block_sum<kThreads>(ssq, red);
+  if (threadIdx.x == 0) partials[t * blocks + b] = s;
+}
+
+__global__ __launch_bounds__(kThreads) void tile_scale_kernel(const float* __restrict__ partials,
+                                                             int per_tile, int64_t n_tiles,
+                                                             float eps, float* __restrict__ inv) {
+  const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= n_tiles) return;
+  float s = 0.f;
+  for (int q = 0; q < per_tile; ++q) s += partials[t * per_tile + q];
+  inv[t] = 1.0f / (sqrtf(s) + eps);
+}
+
+// ---------------------------------------------------------------------------
+// Untile, plain tiles: update[pr, pc] = scale * NS(i, j).
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(kThreads) void untile_plain_kernel(
+    const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
+    const uint16_t* __restrict__ tiles) {
+  const int slabs = geo.mp / kSlabRows;
+  const int64_t item = xcd_item(n_tiles * slabs);
+  if (item >= n_tiles * slabs) return;
+  const int64_t t = item / slabs;
+  const int q = (int)(item % slabs);
+  const HimuonParamDesc& P = params[find_param(params, n_params, t)];
+  const int64_t lt = t - P.tile0;
+  const int r = (int)(lt / P.C), c = (int)(lt % P.C);
+  const float sc = P.upd_scale;
+  const int vpr = geo.np / 8;
+  const uint16_t* in = tiles + t * (int64_t)geo.mp * geo.np;
+  // Only NS columns < tile_w hold data.
+  const int vcols = (geo.tile_w + 7) / 8;
+  for (int v = threadIdx.x; v < kSlabRows * vcols; v += kThreads) {
+    const int i = q * kSlabRows + v / vcols;
+    const int j0 = (v % vcols) * 8;
+    const int64_t pr = (int64_t)r * geo.tile_h + i;
+    const int64_t pc = (int64_t)c * geo.tile_w + j0;
+    if (i >= geo.tile_h || pr >= P.h || pc >= P.w) continue;
+    const uint4 qv = *reinterpret_cast<const uint4*>(in + (int64_t)i * geo.np + j0);
+    const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
+    float y[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      y[2 * k] = sc * bf16_to_f32(w[k] & 0xffffu);
+      y[2 * k + 1] = sc * __uint_as_float(w[k] & 0xffff0000u);
+    }
+    const int64_t ou = pr * P.ld_upd + pc;
+    if (j0 + 8 <= geo.tile_w && pc + 8 <= P.w && aligned16<DT>(P.update, ou)) {
+      store8<DT>(P.update, ou, y);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (j0 + e < geo.tile_w && pc + e < P.w) store_elem<DT>(P.update, ou + e, y[e]);
+    }
+  }
+  (void)vpr;
+}
+
+// Untile, transposed tiles: update[pr, pc] = scale * NS(pc_local, pr_local).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void untile_trans_kernel(
+    const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
+    const uint16_t* __restrict__ tiles) {
+  __shared__ uint16_t sT[kBlk * kBlkPitch];  // [tile row tr][tile col tc]
+  const int bi_n = geo.mp / kBlk, bj_n = geo.np / kBlk;
+  const int blocks = bi_n * bj_n;
+  const int64_t item = xcd_item(n_tiles * blocks);
+  if (item >= n_tiles * blocks) return;
+  const int64_t t = item / blocks;
+  const int b = (int)(item % blocks);
+  const int i0 = (b / bj_n) * kBlk, j0 = (b % bj_n) * kBlk;
+  // NS rows i0.. are tile cols; NS cols j0.. are tile rows. Skip pure padding.
+  if (i0 >= geo.tile_w || j0 >= geo.tile_h) return;
+  const HimuonParamDesc& P = params[find_param(params, n_params, t)];
+  const int64_t lt = t - P.tile0;
+  const int r = (int)(lt / P.C), c = (int)(lt % P.C);
+  const uint16_t* in = tiles + t * (int64_t)geo.mp * geo.np;
+  for (int v = threadIdx.x; v < kBlk * (kBlk / 8); v += kThreads) {
+    const int ii = v / (kBlk / 8), jv = v % (kBlk / 8);
+    const uint4 q = *reinterpret_cast<const uint4*>(in + (int64_t)(i0 + ii) * geo.np + j0 + jv * 8);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      sT[(jv * 8 + 2 * k) * kBlkPitch + ii] = (uint16_t)(w[k] & 0xffffu);
+      sT[(jv * 8 + 2 * k + 1) * kBlkPitch + ii] = (uint16_t)(w[k] >> 16);
+    }
+  }
+  __syncthreads();
+  const float sc = P.upd_scale;
+  for (int v = threadIdx.x; v < kBlk * (kBlk / 8); v += kThreads) {
+    const int rr = v / (kBlk / 8), cv = v % (kBlk / 8);
+    const int tr = j0 + rr, tc = i0 + cv * 8;
+    const int64_t pr = (int64_t)r * geo.tile_h + tr;
+    const int64_t pc = (int64_t)c * geo.tile_w + tc;
+    if (tr >= geo.tile_h || pr >= P.h || tc >= geo.tile_w || pc >= P.w) continue;
+    const uint4 q = *reinterpret_cast<const uint4*>(&sT[rr * kBlkPitch + cv * 8]);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float y[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      y[2 * k] = sc * bf16_to_f32(w[k] & 0xffffu);
+      y[2 * k + 1] = sc * __uint_as_float(w[k] & 0xffff0000u);
+    }
+    const int64_t ou = pr * P.ld_upd + pc;
+    if (tc + 8 <= geo.tile_w && pc + 8 <= P.w && aligned16<DT>(P.update, ou)) {
+      store8<DT>(P.update, ou, y);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (tc + e < geo.tile_w && pc + e < P.w) store_elem<DT>(P.update, ou + e, y[e]);
+    }
+  }
+}
+
+bool geo_ok(int tile_h, int tile_w, int mp, int np) {
+  const int m = tile_h <= tile_w ? tile_h : tile_w;
+  const int n = tile_h <= tile_w ? tile_w : tile_h;
+  return tile_h > 0 && tile_w > 0 && mp >= m && np >= n && mp % HIMUON_NS_ALIGN == 0 &&
+         np % HIMUON_NS_ALIGN == 0;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" int himuon_gather_partials_per_tile(int tile_h, int tile_w, int mp, int np) {
+  if (!geo_ok(tile_h, tile_w, mp, np)) return HIMUON_EINVAL;
+  if (tile_h > tile_w) return (mp / kBlk) * (np / kBlk);
+  return mp / kSlabRows;
+}
+
+extern "C" int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_params,
+                                      int64_t n_tiles, int tile_h, int tile_w, int mp, int np,
+                                      int dtype, uint16_t* tiles_bf16, float* partials,
+                                      void* stream) {
+  if (!geo_ok(tile_h, tile_w, mp, np) || n_params <= 0 || n_tiles < 0 || !params_dev ||
+      !tiles_bf16 || !partials)
+    return HIMUON_EINVAL;
+  if (n_tiles == 0) return 0;
+  const Geo geo{tile_h, tile_w, mp, np};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool trans = tile_h > tile_w;
+  const int64_t items = n_tiles * himuon_gather_partials_per_tile(tile_h, tile_w, mp, np);
+  const dim3 grid((unsigned)xcd_grid(items)), block(kThreads);
+#define HM_GATHER(DT)                                                                         \
+  if (trans)                                                                                  \
+    hipLaunchKernelGGL(gather_trans_kernel<DT>, grid, block, 0, s, params_dev, n_params,       \
+                       n_tiles, geo, tiles_bf16, partials);                     \
+  else                                                                                        \
+    hipLaunchKernelGGL(gather_plain_kernel<DT>, grid, block, 0, s, params_dev, n_params,       \
+                       n_tiles, geo, tiles_bf16, partials);
+  switch (dtype) {
+    case HIMUON_DTYPE_F32: HM_GATHER(HIMUON_DTYPE_F32); break;
+    case HIMUON_DTYPE_BF16: HM_GATHER(HIMUON_DTYPE_BF16); break;
+    case HIMUON_DTYPE_F16: HM_GATHER(HIMUON_DTYPE_F16); break;
+    default: return HIMUON_EINVAL;
+  }
+#undef HM_GATHER
+  return (int)hipGetLastError();
+}
+
+extern "C" int himuon_tile_scale(const float* partials, int partials_per_tile, int64_t n_tiles,
+                                 float eps, float* inv, void* stream) {
+  if (!partials || !inv || partials_per_tile <= 0 || n_tiles < 0) return HIMUON_EINVAL;
+  if (n_tiles == 0) return 0;
+  const dim3 grid((unsigned)((n_tiles + kThreads - 1) / kThreads)), block(kThreads);
+  hipLaunchKernelGGL(tile_scale_kernel, grid, block, 0, static_cast<hipStream_t>(stream),
+                     partials, partials_per_tile, n_tiles, eps, inv);
+  return (int)hipGetLastError();
+}
+
+extern "C" int himuon_untile(const HimuonParamDesc* params_dev, int n_params, int64_t n_tiles,
+                             int tile_h, int tile_w, int mp, int np, int dtype,
+                             const uint16_t* tiles_bf16, void* stream) {
+  if (!geo_ok(tile_h, tile_w, mp, np) || n_params <= 0 || n_tiles < 0 || !params_dev ||
+      !tiles_bf16)
+    return HIMUON_EINVAL;
+  if (n_tiles == 0) return 0;
+  const Geo geo{tile_h, tile_w, mp, np};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool trans = tile_h > tile_w;
+  const int64_t items = n_tiles * himuon_gather_partials_per_tile(tile_h, tile_w, mp, np);
+  const dim3 grid((unsigned)xcd_grid(items)), block(kThreads);
+#define HM_UNTILE(DT)                                                                           \
+  if (trans)                                                                                    \
+    hipLaunchKernelGGL(untile_trans_kernel<DT>, grid, block, 0, s, params_dev, n_params, n_tiles, \
+                       geo, tiles_bf16);                                                         \
+  else                                                                                          \
+    hipLaunchKernelGGL(untile_plain_kernel<DT>, grid, block, 0, s, params_dev, n_params, n_tiles, \
+                       geo, tiles_bf16);
+  switch (dtype) {
+    case HIMUON_DTYPE_F32: HM_UNTILE(HIMUON_DTYPE_F32); break;
+    case HIMUON_DTYPE_BF16: HM_UNTILE(HIMUON_DTYPE_BF16); break;
+    case HIMUON_DTYPE_F16: HM_UNTILE(HIMUON_DTYPE_F16); break;
+    default: return HIMUON_EINVAL;
+  }
+#undef HM_UNTILE
+  return (int)hipGetLastError();
+}

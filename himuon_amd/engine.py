@@ -1,0 +1,160 @@
+"""Device state and launch sequence for one group of same-geometry NS tiles.
+
+A ``TileGroup`` owns everything one bucket of the HiMuon step needs on the
+device, allocated once so pointers stay stable for hipGraph capture:
+
+* the bf16 NS tile buffer ``(n_tiles, mp, np)`` (the concat buffer of
+  himuon.py:588-612, stored directly as the bf16 NS operand),
+* the per-tile sum-of-squares partials and normalisers,
+* the per-parameter ``update`` tensors (grad dtype) the untile kernel writes,
+* the device descriptor table (HimuonParamDesc[]) the gather/untile kernels read.
+
+``run()`` issues: momentum+gather -> tile scale -> NS5 per chunk -> untile.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+
+class TileGroup:
+    def __init__(
+        self,
+        params: list[torch.Tensor],
+        grads: list[torch.Tensor],
+        moms: list[torch.Tensor | None],
+        tile_h: int,
+        tile_w: int,
+        upd_scales: list[float],
+        mus: list[float],
+        nesterovs: list[bool],
+        device: torch.device,
+        dtype: torch.dtype,
+    ):
+        self.tile_h, self.tile_w = int(tile_h), int(tile_w)
+        self.m, self.n, self.mp, self.np, self.trans = nat.ns_geometry(self.tile_h, self.tile_w)
+        self.device = device
+        self.dtype = dtype
+        self.params = params
+        counts = []
+        for g in grads:
+            h, w = g.shape
+            counts.append(((h + self.tile_h - 1) // self.tile_h) * ((w + self.tile_w - 1) // self.tile_w))
+        self.tile_counts = counts
+        self.tile0 = [sum(counts[:i]) for i in range(len(counts))]
+        self.n_tiles = sum(counts)
+        self.ppt = nat.gather_partials_per_tile(self.tile_h, self.tile_w, self.mp, self.np)
+        self.tiles = torch.empty((self.n_tiles, self.mp, self.np), device=device, dtype=torch.bfloat16)
+        self.partials = torch.empty((self.n_tiles, self.ppt), device=device, dtype=torch.float32)
+        self.inv = torch.empty((self.n_tiles,), device=device, dtype=torch.float32)
+        self.updates = [torch.empty(g.shape, device=device, dtype=dtype) for g in grads]
+        self.upd_scales = list(upd_scales)
+        self._sig = None
+        self.desc = None
+        self.bind(grads, moms, mus, nesterovs)
+
+    # -- descriptors -----------------------------------------------------
+    @staticmethod
+    def _check_tensor(t: torch.Tensor, what: str) -> None:
+        if t.ndim != 2:
+            raise ValueError(f"{what} must be 2-D, got shape {tuple(t.shape)}")
+        if t.stride(1) != 1 and t.shape[1] > 1:
+            raise ValueError(f"{what} must be row-major (stride(1) == 1), got strides {t.stride()}")
+
+    def bind(self, grads, moms, mus, nesterovs) -> bool:
+        """(Re)build the device descriptor table if any pointer or momentum
+        setting changed. Returns True if a new table was uploaded."""
+        sig = tuple(
+            (g.data_ptr(), None if m is None else m.data_ptr(), float(mu), bool(nv))
+            for g, m, mu, nv in zip(grads, moms, mus, nesterovs)
+        )
+        if sig == self._sig:
+            return False
+        descs = []
+        for i, (g, m) in enumerate(zip(grads, moms)):
+            self._check_tensor(g, "grad")
+            if g.dtype != self.dtype:
+                raise TypeError(f"bucket dtype {self.dtype} but grad dtype {g.dtype}")
+            if m is not None:
+                self._check_tensor(m, "momentum buffer")
+            u = self.updates[i]
+            h, w = g.shape
+            d = nat.ParamDesc()
+            d.grad = g.data_ptr()
+            d.momentum = m.data_ptr() if m is not None else None
+            d.update = u.data_ptr()
+            d.h, d.w = h, w
+            d.ld_grad = g.stride(0) if h > 1 else w
+            d.ld_mom = (m.stride(0) if h > 1 else w) if m is not None else 0
+            d.ld_upd = u.stride(0) if h > 1 else w
+            d.tile0 = self.tile0[i]
+            d.R = (h + self.tile_h - 1) // self.tile_h
+            d.C = (w + self.tile_w - 1) // self.tile_w
+            d.upd_scale = self.upd_scales[i]
+            d.mu = float(mus[i])
+            d.nesterov = 1 if nesterovs[i] else 0
+            descs.append(d)
+        self.desc = nat.make_desc_table(descs, self.device)
+        self._sig = sig
+        return True
+
+    # -- launches ----------------------------------------------------------
+    def gather(self) -> None:
+        nat.momentum_gather(
+            self.desc, len(self.updates), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
+            self.dtype, self.tiles, self.partials,
+        )
+        nat.tile_scale(self.partials, self.ppt, self.n_tiles, self.inv)
+
+    def ns(self, start: int, count: int, steps: int, workspace: torch.Tensor, sub_batch: int) -> None:
+        if count <= 0:
+            return
+        view = self.tiles[start : start + count]
+        nat.ns5(view, view, self.inv[start : start + count], count, self.mp, self.np, steps, workspace, sub_batch)
+
+    def untile(self) -> None:
+        nat.untile(
+            self.desc, len(self.updates), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
+            self.dtype, self.tiles,
+        )
+
+    def workspace_bytes(self, sub_batch: int) -> int:
+        return nat.ns5_workspace_bytes(sub_batch, self.mp, self.np)
+
+    def default_sub_batch(self) -> int:
+        return nat.default_sub_batch(self.n_tiles, self.mp, self.np)
+
+
+def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
+    """Batched NS5 of ``G`` (..., M, N) on the HIP path; same shape and dtype.
+
+    The batch is viewed as one (B*M, N) matrix cut into M x N tiles, so the
+    gather/untile kernels handle the cast, the transpose-if-tall and the
+    padding (himuon.py:263-284, test_kernels.py:176-198)."""
+    assert G.ndim >= 2
+    if not G.is_cuda:
+        raise RuntimeError("HiMuon.newton_schulz runs on the HIP device only (no CPU path)")
+    M, N = G.shape[-2], G.shape[-1]
+    dtype = G.dtype if G.dtype in nat.DTYPE_CODES else torch.float32
+    flat = G.reshape(-1, M, N).to(dtype).contiguous().view(-1, N)
+    grp = TileGroup(
+        params=[flat],
+        grads=[flat],
+        moms=[None],
+        tile_h=M,
+        tile_w=N,
+        upd_scales=[1.0],
+        mus=[0.0],
+        nesterovs=[False],
+        device=G.device,
+        dtype=dtype,
+    )
+    out = grp.updates[0]
+    sb = grp.default_sub_batch()
+    ws = torch.empty(max(1, grp.workspace_bytes(sb)), device=G.device, dtype=torch.uint8)
+    grp.gather()
+    grp.ns(0, grp.n_tiles, steps, ws, sb)
+    grp.untile()
+    return out.view(G.shape).to(G.dtype)

@@ -1,0 +1,535 @@
+"""HiMuon optimizer on MI355X: the reference's public surface over HIP kernels.
+
+Drop-in for ``tang0389/himuon`` ``src/himuon/optimizers/himuon.py``: same
+constructor signature and defaults (himuon.py:64-80), param-group keys,
+``tile_size`` normalisation (173-179), ``reconfigure`` (188-213),
+``xlayer_plan`` (407-415), plan dicts (483-586), ``_balanced_chunks``
+(459-481), ``_auto_b_hw`` (376-403), graph warm-up / capture / replay state
+machine (1048-1109) with LR and weight decay applied outside the graph
+(215-228), and ``newton_schulz`` (263-284).
+
+What changes is the GPU body of a step. Per bucket of same-shape tiles the
+step issues one fused momentum+gather launch, one normaliser launch, the NS5
+launches per chunk and one untile launch (libhimuon_hip.so, C ABI in
+include/himuon_hip.h) instead of per-parameter torch/inductor/Triton ops.
+Full-matrix (numel <= tile area) parameters of equal shape are batched into
+one NS group instead of one NS call per parameter (himuon.py:827-876); the
+math per matrix is unchanged.
+
+There is no CPU path: ``step()`` on non-HIP tensors raises, as the
+reference's does without its GPU kernels (triton_kernels/__init__.py:8-19).
+FSDP/DTensor parameters (himuon.py:419-457, 894-1020) are out of scope.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+from torch.optim import Optimizer
+
+from .. import _native as nat
+from ..engine import TileGroup
+from ..engine import newton_schulz as _hip_newton_schulz
+
+try:
+    from torch.distributed.tensor import DTensor as _DTensor  # type: ignore
+except Exception:  # pragma: no cover
+    _DTensor = None  # type: ignore
+
+
+class HiMuon(Optimizer):
+    """Hierarchical Muon with cross-layer batched NS on HIP kernels.
+
+    Args (identical to the reference, himuon.py:48-62):
+        params: model parameters
+        lr: learning rate (default 0.02)
+        momentum: momentum coefficient (default 0.95)
+        nesterov: use Nesterov momentum (default True)
+        weight_decay: weight decay (default 0.1)
+        tile_size: int -> (T, T) tiles; (Th, Tw) -> non-square tiles (default 512)
+        ns_steps: Newton-Schulz iterations (default 5)
+        use_muon: Muon path, otherwise AdamW fallback (default True)
+        lr_adjust: "tile" (lr * 0.2 * sqrt(max block dim)) or "none"
+        adamw_betas / adamw_eps: AdamW fallback hyper-parameters
+        b_hw: cross-layer chunk cap (None -> from device memory)
+        cuda_graph: capture the step in a hipGraph after ``cuda_graph_warmup``
+            eager steps (the name is kept for drop-in compatibility).
+    """
+
+    def __init__(
+        self,
+        params,
+        lr=0.02,
+        momentum=0.95,
+        nesterov=True,
+        weight_decay=0.1,
+        tile_size=512,
+        ns_steps=5,
+        use_muon=True,
+        lr_adjust="tile",
+        adamw_betas=(0.95, 0.95),
+        adamw_eps=1e-8,
+        b_hw=None,
+        cuda_graph=True,
+        cuda_graph_warmup=3,
+    ):
+        tile_size = self._normalize_defaults(tile_size)
+        defaults = dict(
+            lr=lr,
+            momentum=momentum,
+            nesterov=nesterov,
+            weight_decay=weight_decay,
+            tile_size=tile_size,
+            ns_steps=ns_steps,
+            use_muon=use_muon,
+            adamw_betas=adamw_betas,
+            adamw_eps=adamw_eps,
+        )
+        super().__init__(params, defaults)
+
+        self._b_hw_override = b_hw
+        self._memory_budget_fraction = 0.15
+        # bucket_key -> bf16 NS tile buffer (n_tiles, mp, np) of that bucket.
+        self._concat_buffers: dict[tuple, torch.Tensor] = {}
+        self._cached_plan: "list[dict] | None" = None
+        self._last_step_stats: dict = {"ns_gpu_ms": 0.0, "ns_launches": 0, "total_B": 0, "avg_batch": 0.0}
+
+        self._cuda_graph_enabled = bool(cuda_graph)
+        self._cuda_graph_warmup = int(cuda_graph_warmup)
+        self._cuda_graph: "torch.cuda.CUDAGraph | None" = None
+        self._graph_step_count: int = 0
+        self._in_graph_region: bool = False
+        # (param, update_tensor, group_idx), filled at capture, applied after replay.
+        self._pending_updates: list[tuple] = []
+
+        # Device state of the HIP path, rebuilt after reconfigure().
+        self._groups: "list[dict] | None" = None  # tiled buckets + full-NS shape groups
+        self._workspace: "torch.Tensor | None" = None
+
+        if lr_adjust not in ("none", "tile"):
+            raise ValueError(f"lr_adjust must be 'none' or 'tile', got {lr_adjust!r}")
+        self.lr_adjust = lr_adjust
+
+    # -- Reconfiguration (himuon.py:173-228) --------------------------------
+
+    @staticmethod
+    def _normalize_defaults(tile_size):
+        if isinstance(tile_size, int):
+            tile_size = (tile_size, tile_size)
+        tile_size = tuple(tile_size)
+        assert len(tile_size) == 2 and all(t > 0 for t in tile_size)
+        return tile_size
+
+    def adjust_lr_for_muon(self, lr, block_shape):
+        """Adapted from Muon's adjust_lr_for_muon."""
+        if self.lr_adjust == "none":
+            return lr
+        a, b = block_shape[:2]
+        return lr * 0.2 * math.sqrt(max(a, b))
+
+    def reconfigure(self, **updates):
+        """Update param-group defaults mid-training (e.g., tile_size) and drop
+        the cached plan, buffers and captured graph."""
+        for group in self.param_groups:
+            ts = self._normalize_defaults(updates.get("tile_size", group["tile_size"]))
+            for k, v in updates.items():
+                if k in group:
+                    group[k] = v
+            if "tile_size" in updates:
+                group["tile_size"] = ts
+        self._invalidate_plan_cache()
+
+    def _invalidate_plan_cache(self):
+        """Flush plan, tile buffers, device state, graph and pending updates.
+        (The reference also resets torch._dynamo for its compiled helpers; this
+        path compiles nothing at run time.)"""
+        self._concat_buffers.clear()
+        self._cached_plan = None
+        self._groups = None
+        self._workspace = None
+        self._cuda_graph = None
+        self._graph_step_count = 0
+        self._pending_updates.clear()
+
+    def _apply_pending_updates(self):
+        """WD + LR application after replay, reading the current group lr/wd."""
+        for p, update, group_idx in self._pending_updates:
+            group = self.param_groups[group_idx]
+            lr = group["lr"]
+            weight_decay = group["weight_decay"]
+            if weight_decay > 0.0:
+                p.data.mul_(1 - lr * weight_decay)
+            p.data.add_(update, alpha=-lr)
+
+    # -- Newton-Schulz --------------------------------------------------------
+
+    @staticmethod
+    def newton_schulz(G, steps=5):
+        """Quintic NS of G (..., M, N) on the HIP kernels; returns G's shape and
+        dtype (himuon.py:263-284). ``steps`` is honoured for every shape."""
+        return _hip_newton_schulz(G, steps=steps)
+
+    # -- Tiling helpers (himuon.py:288-310), torch views only ---------------
+
+    @staticmethod
+    def _tile(tensor, tile_size):
+        """Tile (H, W) -> (R, C, Th, Tw) with zero-padding."""
+        tile_h, tile_w = tile_size
+        h, w = tensor.shape
+        pad_h = (tile_h - h % tile_h) % tile_h
+        pad_w = (tile_w - w % tile_w) % tile_w
+        if pad_h or pad_w:
+            tensor = torch.nn.functional.pad(tensor, (0, pad_w, 0, pad_h))
+        H, W = tensor.shape
+        R, C = H // tile_h, W // tile_w
+        return tensor.view(R, tile_h, C, tile_w).permute(0, 2, 1, 3).contiguous(), (h, w, pad_h, pad_w)
+
+    @staticmethod
+    def _untile(tiled, info):
+        """Restore (R, C, Th, Tw) -> (H, W) and remove padding."""
+        h, w, pad_h, pad_w = info
+        R, C, Th, Tw = tiled.shape
+        restored = tiled.permute(0, 2, 1, 3).contiguous().view(R * Th, C * Tw)
+        return restored[:h, :w] if (pad_h or pad_w) else restored
+
+    # -- AdamW fallback (himuon.py:359-372, 878-888) --------------------------
+
+    def _compute_adamw_step(self, p, g, betas, eps):
+        if "step" not in self.state[p]:
+            self.state[p]["step"] = torch.zeros((), device=g.device)
+            self.state[p]["moment1"] = torch.zeros_like(g)
+            self.state[p]["moment2"] = torch.zeros_like(g)
+        step = self.state[p]["step"]
+        step.add_(1)
+        buf1, buf2 = self.state[p]["moment1"], self.state[p]["moment2"]
+        buf1.lerp_(g, 1 - betas[0])
+        buf2.lerp_(g.square(), 1 - betas[1])
+        bc1 = 1 - betas[0] ** step
+        bc2 = 1 - betas[1] ** step
+        return (buf1 / bc1) / (buf2.sqrt() / bc2**0.5 + eps)
+
+    def _apply_wd_and_update(self, p, update, weight_decay, lr, group_idx, scaled=False):
+        """Graph region: defer to _apply_pending_updates. Eager: apply now.
+        ``update`` from the HIP path already carries the lr-adjust scale."""
+        if self._in_graph_region:
+            self._pending_updates.append((p, update, group_idx))
+        else:
+            if weight_decay > 0.0:
+                p.data.mul_(1 - lr * weight_decay)
+            p.data.add_(update, alpha=-lr)
+
+    def _step_adamw(self, group, group_idx):
+        lr = group["lr"]
+        weight_decay = group["weight_decay"]
+        for p in group["params"]:
+            if p.grad is None:
+                continue
+            update = self._compute_adamw_step(p, p.grad, group["adamw_betas"], group["adamw_eps"])
+            self._apply_wd_and_update(p, update, weight_decay, lr, group_idx)
+
+    # -- Chunk cap and plan (himuon.py:376-415, 459-586) ---------------------
+
+    def _auto_b_hw(self, T: int, dtype_bytes: int = 4) -> int:
+        if not torch.cuda.is_available():
+            user = self._b_hw_override
+            return max(1, int(user)) if user is not None else 1
+        device = torch.cuda.current_device()
+        total_mem = torch.cuda.get_device_properties(device).total_memory
+        budget = int(self._memory_budget_fraction * total_mem)
+        bytes_per_tile = 4 * T * T * dtype_bytes
+        mem_cap = max(1, budget // bytes_per_tile)
+        if self._b_hw_override is not None:
+            return max(1, min(int(self._b_hw_override), mem_cap))
+        return mem_cap
+
+    def xlayer_plan(self) -> list[dict]:
+        if self._cached_plan is None:
+            return []
+        return list(self._cached_plan)
+
+    def _is_dtensor(self, p) -> bool:
+        return _DTensor is not None and isinstance(p, _DTensor)
+
+    @staticmethod
+    def _balanced_chunks(B_total: int, b_hw: int) -> list[int]:
+        """ceil(B_total / b_hw) chunks of ceil(remaining / remaining_chunks)."""
+        if B_total <= 0:
+            return []
+        n_chunks = math.ceil(B_total / b_hw)
+        chunks: list[int] = []
+        remaining = B_total
+        for i in range(n_chunks):
+            c = math.ceil(remaining / (n_chunks - i))
+            chunks.append(c)
+            remaining -= c
+        return chunks
+
+    def _plan_buckets(self) -> list[dict]:
+        """Tiled buckets keyed (tile_h, tile_w, False, grad dtype) in
+        param_groups/params order; params with numel <= tile area are left to
+        the full-NS path (himuon.py:541-544)."""
+        by_key: dict[tuple, list] = {}
+        for group in self.param_groups:
+            if not group["use_muon"]:
+                continue
+            tile_h, tile_w = group["tile_size"]
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                if self._is_dtensor(p):
+                    raise NotImplementedError(
+                        "HiMuon (HIP path) runs on one GPU; FSDP/DTensor parameters are not supported"
+                    )
+                grad = p.grad
+                if grad.numel() <= tile_h * tile_w:
+                    continue
+                h, w = grad.shape
+                R = -(-h // tile_h)
+                C = -(-w // tile_w)
+                key = (tile_h, tile_w, False, grad.dtype)
+                by_key.setdefault(key, []).append((p, group, R * C))
+
+        plan: list[dict] = []
+        for key, entries in by_key.items():
+            tile_h, tile_w, _full_ns, _dtype = key
+            T = max(tile_h, tile_w)
+            dtype_bytes = torch.empty((), dtype=_dtype).element_size()
+            b_hw = self._auto_b_hw(T, dtype_bytes=dtype_bytes)
+            tile_count_per_param = [e[2] for e in entries]
+            B_total = sum(tile_count_per_param)
+            chunk_sizes = self._balanced_chunks(B_total, b_hw)
+            plan.append(
+                {
+                    "bucket_key": key,
+                    "param_ids": [id(e[0]) for e in entries],
+                    "tile_count_per_param": tile_count_per_param,
+                    "B_total": B_total,
+                    "B_hw": b_hw,
+                    "chunk_sizes": chunk_sizes,
+                    "n_calls": len(chunk_sizes),
+                    "_entries": entries,
+                }
+            )
+        return plan
+
+    def _plan_full_ns(self) -> list[dict]:
+        """Full-NS parameters (numel <= tile area) grouped by (shape, dtype,
+        ns_steps), in param_groups/params order."""
+        by_key: dict[tuple, list] = {}
+        for group in self.param_groups:
+            if not group["use_muon"]:
+                continue
+            tile_h, tile_w = group["tile_size"]
+            for p in group["params"]:
+                if p.grad is None or self._is_dtensor(p):
+                    continue
+                if p.grad.numel() > tile_h * tile_w:
+                    continue
+                if p.grad.ndim != 2:
+                    raise ValueError(f"HiMuon muon params must be 2-D, got {tuple(p.grad.shape)}")
+                key = (tuple(p.grad.shape), p.grad.dtype, group["ns_steps"])
+                by_key.setdefault(key, []).append((p, group))
+        return [{"key": k, "entries": v} for k, v in by_key.items()]
+
+    # -- Device state -----------------------------------------------------------
+
+    def _momentum_buffer(self, p):
+        st = self.state[p]
+        if "momentum_buffer" not in st:
+            st["momentum_buffer"] = torch.zeros_like(p.grad)
+        return st["momentum_buffer"]
+
+    def _build_groups(self, plan: list[dict]) -> list[dict]:
+        group_to_idx = {id(g): i for i, g in enumerate(self.param_groups)}
+        out = []
+        for bucket in plan:
+            tile_h, tile_w, _f, dtype = bucket["bucket_key"]
+            entries = bucket["_entries"]
+            steps = {e[1]["ns_steps"] for e in entries}
+            assert len(steps) <= 1, f"cross-layer NS requires a uniform ns_steps per bucket; saw {steps}"
+            params = [e[0] for e in entries]
+            grp = TileGroup(
+                params=params,
+                grads=[p.grad for p in params],
+                moms=[self._momentum_buffer(p) for p in params],
+                tile_h=tile_h,
+                tile_w=tile_w,
+                upd_scales=[self.adjust_lr_for_muon(1.0, (tile_h, tile_w))] * len(params),
+                mus=[e[1]["momentum"] for e in entries],
+                nesterovs=[e[1]["nesterov"] for e in entries],
+                device=params[0].grad.device,
+                dtype=dtype,
+            )
+            self._concat_buffers[bucket["bucket_key"]] = grp.tiles
+            out.append(
+                {
+                    "tiles": grp,
+                    "entries": [(p, g) for p, g, _ in entries],
+                    "group_idx": [group_to_idx[id(g)] for _, g, _ in entries],
+                    "steps": next(iter(steps)) if steps else 5,
+                    "chunks": list(bucket["chunk_sizes"]),
+                    "full": False,
+                }
+            )
+        for fg in self._plan_full_ns():
+            (h, w), dtype, steps = fg["key"]
+            entries = fg["entries"]
+            params = [p for p, _ in entries]
+            # One tile per matrix: tile = (h, w); lr scale from p.shape (himuon.py:872-874).
+            grp = TileGroup(
+                params=params,
+                grads=[p.grad for p in params],
+                moms=[self._momentum_buffer(p) for p in params],
+                tile_h=h,
+                tile_w=w,
+                upd_scales=[self.adjust_lr_for_muon(1.0, p.shape) for p in params],
+                mus=[g["momentum"] for _, g in entries],
+                nesterovs=[g["nesterov"] for _, g in entries],
+                device=params[0].grad.device,
+                dtype=dtype,
+            )
+            out.append(
+                {
+                    "tiles": grp,
+                    "entries": entries,
+                    "group_idx": [group_to_idx[id(g)] for _, g in entries],
+                    "steps": steps,
+                    "chunks": [grp.n_tiles],
+                    "full": True,
+                }
+            )
+        # One NS workspace shared by all groups, sized for the largest need.
+        need = 1
+        for g in out:
+            grp = g["tiles"]
+            g["sub_batch"] = grp.default_sub_batch()
+            need = max(need, grp.workspace_bytes(g["sub_batch"]))
+        device = out[0]["tiles"].device if out else None
+        if device is not None and (self._workspace is None or self._workspace.numel() < need):
+            self._workspace = torch.empty(need, device=device, dtype=torch.uint8)
+        return out
+
+    def _ensure_device_state(self):
+        if self._cached_plan is None:
+            self._cached_plan = self._plan_buckets()
+            self._groups = None
+        if self._groups is None:
+            self._groups = self._build_groups(self._cached_plan)
+        else:
+            # Eager steps re-bind if grads/momentum moved or momentum settings changed.
+            for g in self._groups:
+                params = [p for p, _ in g["entries"]]
+                g["tiles"].bind(
+                    [p.grad for p in params],
+                    [self._momentum_buffer(p) for p in params],
+                    [grp["momentum"] for _, grp in g["entries"]],
+                    [grp["nesterov"] for _, grp in g["entries"]],
+                )
+        return self._groups
+
+    # -- Step body ----------------------------------------------------------------
+
+    def _has_dtensor_muon(self) -> bool:
+        for g in self.param_groups:
+            if not g["use_muon"]:
+                continue
+            for p in g["params"]:
+                if p.grad is not None and self._is_dtensor(p):
+                    return True
+        return False
+
+    def _run_groups(self, groups) -> dict:
+        use_events = not self._in_graph_region
+        ev_pairs = []
+        ns_launches = 0
+        total_B = 0
+        for g in groups:
+            grp: TileGroup = g["tiles"]
+            grp.gather()
+            ofs = 0
+            for c in g["chunks"]:
+                if use_events:
+                    ev0 = torch.cuda.Event(enable_timing=True)
+                    ev1 = torch.cuda.Event(enable_timing=True)
+                    ev0.record()
+                grp.ns(ofs, c, g["steps"], self._workspace, g["sub_batch"])
+                if use_events:
+                    ev1.record()
+                    ev_pairs.append((ev0, ev1))
+                ns_launches += 1
+                total_B += c
+                ofs += c
+            grp.untile()
+            for (p, grp_dict), gi, upd in zip(g["entries"], g["group_idx"], grp.updates):
+                self._apply_wd_and_update(p, upd, grp_dict["weight_decay"], grp_dict["lr"], gi)
+        ns_ms = 0.0
+        if use_events and ev_pairs:
+            ev_pairs[-1][1].synchronize()
+            ns_ms = sum(a.elapsed_time(b) for a, b in ev_pairs)
+        return {"ns_gpu_ms": ns_ms, "ns_launches": ns_launches, "total_B": total_B}
+
+    def _step_body(self):
+        """Momentum -> tile -> NS5 -> untile for every muon param (HIP), then the
+        AdamW groups (torch), with WD/LR applied eagerly or deferred to after
+        graph replay."""
+        if self._has_dtensor_muon():
+            raise NotImplementedError("HiMuon (HIP path) runs on one GPU; FSDP/DTensor parameters are not supported")
+        groups = self._ensure_device_state()
+        stats = self._run_groups(groups) if groups else {"ns_gpu_ms": 0.0, "ns_launches": 0, "total_B": 0}
+        for group_idx, group in enumerate(self.param_groups):
+            if not group["use_muon"]:
+                self._step_adamw(group, group_idx)
+        n = stats["ns_launches"]
+        self._last_step_stats = {
+            "ns_gpu_ms": float(stats["ns_gpu_ms"]),
+            "ns_launches": int(n),
+            "total_B": int(stats["total_B"]),
+            "avg_batch": float(stats["total_B"]) / float(n) if n > 0 else 0.0,
+        }
+
+    def _check_device(self):
+        for g in self.param_groups:
+            for p in g["params"]:
+                if p.grad is not None and not p.grad.is_cuda:
+                    raise RuntimeError(
+                        "HiMuon (HIP path) requires parameters and grads on a ROCm device; "
+                        "there is no CPU implementation of step()"
+                    )
+
+    def _capture_graph(self) -> None:
+        """Capture momentum..untile into a hipGraph; WD/LR stay outside."""
+        self._ensure_device_state()  # allocate everything before capture
+        torch.cuda.synchronize()
+        self._pending_updates.clear()
+        self._cuda_graph = torch.cuda.CUDAGraph()
+        self._in_graph_region = True
+        try:
+            with torch.cuda.graph(self._cuda_graph):
+                self._step_body()
+        finally:
+            self._in_graph_region = False
+        self._cuda_graph.replay()
+        self._apply_pending_updates()
+        torch.cuda.synchronize()
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            loss = closure()
+        self._check_device()
+        if not self._cuda_graph_enabled or not torch.cuda.is_available():
+            self._step_body()
+            return loss
+        if self._graph_step_count < self._cuda_graph_warmup:
+            self._step_body()
+            self._graph_step_count += 1
+            return loss
+        if self._cuda_graph is None:
+            self._capture_graph()
+            return loss
+        self._cuda_graph.replay()
+        self._apply_pending_updates()
+        self._last_step_stats = {"ns_gpu_ms": 0.0, "ns_launches": 0, "total_B": 0, "avg_batch": 0.0}
+        return loss

@@ -1,0 +1,158 @@
+/*
+ * himuon_hip.h — C ABI of libhimuon_hip.so, the MI355X (gfx950) kernels behind
+ * the HiMuon optimizer step.
+ *
+ * The library replaces the GPU bodies of the reference optimizer's step
+ * (tang0389/himuon, src/himuon/optimizers/himuon.py). Host code (Python/ctypes
+ * in himuon_amd/_native.py) owns every buffer; nothing here allocates device
+ * memory, synchronises the device or keeps mutable global state, so every entry
+ * point may be recorded into a hipGraph. All launches go to the caller's
+ * stream. All entry points return 0 on success, a positive hipError_t from the
+ * launch, or a negative HIMUON_E* code for an argument error found on the host
+ * before anything was launched.
+ *
+ * Data layout shared by the entry points
+ * --------------------------------------
+ *  Bucket geometry: every parameter of a bucket is cut into tile_h x tile_w
+ *  tiles (zero padded at the bottom/right edge of the parameter). A tile is
+ *  "transposed" when tile_h > tile_w: the Newton-Schulz (NS) operand is then
+ *  the tile's transpose, so NS always sees an m x n matrix with m <= n,
+ *  m = min(tile_h, tile_w), n = max(tile_h, tile_w).
+ *
+ *  NS tile buffer: bf16, shape (n_tiles, mp, np) row-major, mp >= m and
+ *  np >= n multiples of HIMUON_NS_ALIGN. NS tile t holds the tile at
+ *  bucket tile index t in its top-left m x n corner and zeros elsewhere
+ *  (zero rows/columns stay exactly zero through NS).
+ *
+ *  Tile numbering: parameter p owns tiles [tile0_p, tile0_p + R_p*C_p); tile
+ *  (r, c) of the parameter's R_p x C_p tile grid is tile0_p + r*C_p + c
+ *  (row-major), the concat-buffer order of himuon.py:677-719.
+ */
+#ifndef HIMUON_HIP_H
+#define HIMUON_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HIMUON_ABI_VERSION 1
+
+/* Element type codes for gradients / momentum / updates. */
+#define HIMUON_DTYPE_F32 0
+#define HIMUON_DTYPE_BF16 1
+#define HIMUON_DTYPE_F16 2
+
+/* NS tile buffer dimensions (mp, np) must be multiples of this. */
+#define HIMUON_NS_ALIGN 128
+
+/* Host-side argument errors (negative return codes). */
+#define HIMUON_EINVAL (-22)
+#define HIMUON_ENOSPC (-28)
+
+/*
+ * One parameter of a bucket. An array of these lives in device memory (built
+ * once per plan by the host) and is read by the gather and untile kernels.
+ * 96 bytes, 8-byte aligned; field order is part of the ABI. Parameters of one
+ * bucket may come from different param groups, so the per-group momentum
+ * settings travel with each parameter.
+ */
+typedef struct HimuonParamDesc {
+  const void* grad;   /* (h, w) gradient, row stride ld_grad elements          */
+  void* momentum;     /* (h, w) momentum buffer, row stride ld_mom; may be NULL */
+  void* update;       /* (h, w) update output, row stride ld_upd                */
+  int64_t h, w;
+  int64_t ld_grad, ld_mom, ld_upd;
+  int64_t tile0;      /* first NS tile index of this parameter                  */
+  int32_t R, C;       /* tile grid: ceil(h / tile_h) x ceil(w / tile_w)         */
+  float upd_scale;    /* update = upd_scale * NS output (lr adjustment)          */
+  float mu;           /* momentum coefficient                                    */
+  int32_t nesterov;   /* nonzero: Nesterov momentum                              */
+  int32_t reserved;
+} HimuonParamDesc;
+
+/* Library ABI version (HIMUON_ABI_VERSION it was built with). */
+int himuon_abi_version(void);
+
+/* Human-readable text for any return code of this library. */
+const char* himuon_error_string(int code);
+
+/* Number of fp32 sum-of-squares partials himuon_momentum_gather writes per NS
+ * tile for this geometry (the row length of its `partials` output). */
+int himuon_gather_partials_per_tile(int tile_h, int tile_w, int mp, int np);
+
+/*
+ * Fused Nesterov momentum + tile gather + per-tile sum of squares.
+ * Replaces the per-parameter pre-NS loop of himuon.py:696-719
+ * (_compute_momentum himuon.py:350-357, F.pad + permute-copy into the concat
+ * buffer) and the bf16 cast of the NS prologue (himuon.py:239, 274).
+ *
+ * For every element of every parameter (grad g, momentum buf, both in
+ * `dtype`; mu and nesterov from the parameter's descriptor):
+ *     buf <- rd(rd(mu * buf) + g)                      (in place)
+ *     e   <- nesterov ? rd(fma(mu, buf, g)) : buf
+ * (fp32 arithmetic; rd = round to `dtype`; the buf update rounds its product
+ * and sum separately, e is one fused multiply-add, as torch's in-place mul_,
+ * add_ and add(alpha=) evaluate them). If momentum is NULL, e = g and
+ * nothing is written back. bf16(e) is stored at its NS tile position; padding
+ * is written as zero. partials[t * P + q] receives the fp32 sum of squares of
+ * the bf16 values of the q-th slab of NS tile t, P =
+ * himuon_gather_partials_per_tile(...).
+ */
+int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_params,
+                           int64_t n_tiles, int tile_h, int tile_w, int mp,
+                           int np, int dtype, uint16_t* tiles_bf16,
+                           float* partials, void* stream);
+
+/*
+ * Per-tile normaliser: inv[t] = 1 / (sqrt(sum_q partials[t*P+q]) + eps).
+ * The reciprocal of the divisor of himuon.py:242 / ns5_smem.py:84-86
+ * (Frobenius norm of the bf16 tile, fp32).
+ */
+int himuon_tile_scale(const float* partials, int partials_per_tile,
+                      int64_t n_tiles, float eps, float* inv, void* stream);
+
+/* Workspace bytes himuon_ns5 needs for a given sub-batch size. */
+size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np);
+
+/*
+ * Batched quintic Newton-Schulz on n_tiles NS tiles (bf16, (n_tiles, mp, np)).
+ * Replaces HiMuon.newton_schulz / _newton_schulz_3kernel / ns5_smem
+ * (himuon.py:232-284; triton_kernels/XXT.py:13-75, ba_plus_cAA.py:13-89,
+ * fused_bmm_add.py:13-96, ns5_smem.py:46-104).
+ *
+ *   X0 = bf16(x * inv[t])                 (x = tiles_in, i.e. bf16 of the tile)
+ *   repeat `steps` times:
+ *     A = bf16(X X^T)                       fp32 accumulation
+ *     B = bf16(c * (A A^T) + b * A)          fp32 accumulation / epilogue
+ *     X = bf16(bf16(B X) + a * X)
+ *   tiles_out = X
+ *
+ * tiles_out may equal tiles_in. Tiles are processed in sub-batches of
+ * `sub_batch`; the workspace must hold himuon_ns5_workspace_bytes(sub_batch,
+ * mp, np) bytes. steps == 0 writes X0.
+ */
+int himuon_ns5(const uint16_t* tiles_in, uint16_t* tiles_out, const float* inv,
+               int64_t n_tiles, int mp, int np, int steps, float a, float b,
+               float c, void* workspace, size_t workspace_bytes,
+               int64_t sub_batch, void* stream);
+
+/*
+ * Untile/scatter: for every element of every parameter,
+ *     update[row, col] = round_dtype(upd_scale * float(NS tile value))
+ * reading the NS tile position of (row, col) (transposed back when
+ * tile_h > tile_w). Replaces _post_ns_per_param (himuon.py:315-329; _untile
+ * himuon.py:302-310), the NS output cast (himuon.py:257, 283) and the
+ * in-graph `update.mul_(scale)` (himuon.py:338-341).
+ */
+int himuon_untile(const HimuonParamDesc* params_dev, int n_params,
+                  int64_t n_tiles, int tile_h, int tile_w, int mp, int np,
+                  int dtype, const uint16_t* tiles_bf16, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIMUON_HIP_H */

@@ -1,0 +1,91 @@
+"""CPU checks of the C ABI: libhimuon_hip.so loads, exports every function
+include/himuon_hip.h declares, agrees on the descriptor layout, and rejects bad
+arguments on the host before launching anything (no GPU needed)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from himuon_amd import _native as nat
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "himuon_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(himuon_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not nat.lib_path().exists():
+        pytest.fail(f"{nat.lib_path()} missing: run `python -m himuon_amd.build`")
+    return nat.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = _declared_functions()
+    assert declared, "no functions parsed from the header"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(nat.lib_path())], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (himuon_\w+)", out))
+    assert set(declared) <= exported, set(declared) - exported
+    assert set(declared) == set(nat.exported_symbols())
+    for name in declared:
+        assert hasattr(lib, name)
+
+
+def test_abi_version_and_errors(lib):
+    assert lib.himuon_abi_version() == nat.ABI_VERSION
+    assert lib.himuon_error_string(0) == b"success"
+    assert b"invalid" in lib.himuon_error_string(-22)
+    assert b"workspace" in lib.himuon_error_string(-28)
+
+
+def test_desc_layout_matches_header():
+    # offsets of HimuonParamDesc fields (include/himuon_hip.h)
+    d = nat.ParamDesc
+    assert ctypes.sizeof(d) == 96
+    assert d.tile0.offset == 64 and d.R.offset == 72 and d.upd_scale.offset == 80
+    assert d.mu.offset == 84 and d.nesterov.offset == 88
+
+
+def test_partials_per_tile(lib):
+    assert lib.himuon_gather_partials_per_tile(512, 512, 512, 512) == 512 // 32
+    assert lib.himuon_gather_partials_per_tile(1024, 512, 512, 1024) == (512 // 64) * (1024 // 64)
+    assert lib.himuon_gather_partials_per_tile(512, 512, 500, 512) == -22  # not aligned
+    assert lib.himuon_gather_partials_per_tile(512, 512, 384, 512) == -22  # mp < m
+
+
+def test_workspace_bytes(lib):
+    assert lib.himuon_ns5_workspace_bytes(4, 512, 512) == 4 * 4 * 512 * 512 * 2
+    assert lib.himuon_ns5_workspace_bytes(0, 512, 512) == 0
+
+
+def test_argument_errors_return_before_launch(lib):
+    z = None
+    # null descriptor / buffers
+    assert lib.himuon_momentum_gather(z, 1, 4, 512, 512, 512, 512, 0, z, z, z) == -22
+    # bad dtype code with otherwise valid (dummy) pointers: still rejected on the host
+    assert lib.himuon_momentum_gather(8, 1, 4, 512, 512, 512, 512, 9, 8, 8, z) == -22
+    # mp > np is not an NS geometry
+    assert lib.himuon_ns5(8, 8, 8, 4, 1024, 512, 5, 1.0, 1.0, 1.0, 8, 1 << 30, 4, z) == -22
+    # workspace too small
+    assert lib.himuon_ns5(8, 8, 8, 4, 512, 512, 5, 1.0, 1.0, 1.0, 8, 16, 4, z) == -28
+    assert lib.himuon_untile(z, 1, 4, 512, 512, 512, 512, 0, z, z) == -22
+    assert lib.himuon_tile_scale(z, 16, 4, 1e-7, z, z) == -22
+    # empty work is a no-op success
+    assert lib.himuon_tile_scale(8, 16, 0, 1e-7, 8, z) == 0
+
+
+def test_geometry_helpers():
+    assert nat.ns_geometry(512, 512) == (512, 512, 512, 512, False)
+    assert nat.ns_geometry(768, 513) == (513, 768, 640, 768, True)
+    assert nat.ns_geometry(64, 64) == (64, 64, 128, 128, False)
+    assert nat.ns_geometry(1024, 3072) == (1024, 3072, 1024, 3072, False)

@@ -1,0 +1,260 @@
+"""GPU parity of the HIP kernels against the CPU oracle and torch references.
+
+* gather (momentum + tile + bf16 cast): bit-exact momentum buffers and NS tiles
+  against oracle.momentum / oracle.tile, every padding and transpose case;
+* untile: bit-exact updates against oracle.untile times the lr scale;
+* NS5: per-tile relative Frobenius error against the reference's NS5 in the
+  same dtypes (torch on the GPU) and against the CPU oracle, plus the
+  singular-value band of every tile.
+
+Inputs are generated on the CPU from fixed seeds and copied to the device.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import himuon_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from himuon_amd import _native as nat
+    from himuon_amd.engine import TileGroup, newton_schulz
+
+    from gpu_ref import ns5_torch_eager, ns5_torch_staged, per_tile_rel_fro, well_conditioned
+
+DEV = "cuda"
+TDT = {"float32": torch.float32, "bfloat16": torch.bfloat16, "float16": torch.float16}
+
+
+def _cpu_randn(shape, seed, scale=1.0, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def _ns_layout(tiles_hw: np.ndarray, mp: int, np_: int) -> np.ndarray:
+    """(n, Th, Tw) tiles -> (n, mp, np) NS operands (transposed if tall, zero padded)."""
+    n, th, tw = tiles_hw.shape
+    x = np.swapaxes(tiles_hw, 1, 2) if th > tw else tiles_hw
+    out = np.zeros((n, mp, np_), dtype=np.float32)
+    out[:, : x.shape[1], : x.shape[2]] = x
+    return out
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu()
+    if t.dtype == torch.float32:
+        return t.numpy().view(np.uint32)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+GATHER_CASES = [
+    # (name, [param shapes], tile_h, tile_w, dtype, nesterov)
+    ("square_256_fp32", [(1024, 1024)], 256, 256, "float32", True),
+    ("pad_512_fp32", [(768, 513), (513, 768)], 512, 512, "float32", True),
+    ("tall_tiles_fp32", [(300, 200), (128, 64)], 128, 64, "float32", True),
+    ("wide_tiles_bf16", [(200, 300)], 64, 128, "bfloat16", True),
+    ("multi_bf16_plain", [(512, 1024), (256, 512), (1024, 2048)], 256, 256, "bfloat16", False),
+    ("fp16", [(384, 640)], 128, 128, "float16", True),
+    ("full_tall_fp32", [(2048, 1024)], 2048, 1024, "float32", True),
+    ("odd_small", [(7, 50), (50, 7)], 16, 16, "float32", True),
+]
+
+
+def _make_group(shapes, th, tw, dtype, nesterov, seed, mus=None, with_mom=True):
+    tdt = TDT[dtype]
+    grads = [_cpu_randn(s, seed + i, 1e-3, tdt).to(DEV) for i, s in enumerate(shapes)]
+    moms = [_cpu_randn(s, seed + 100 + i, 1e-3, tdt).to(DEV) if with_mom else None for i, s in enumerate(shapes)]
+    mus = mus or [0.95] * len(shapes)
+    grp = TileGroup(
+        params=grads, grads=grads, moms=moms, tile_h=th, tile_w=tw,
+        upd_scales=[O.lr_scale((th, tw))] * len(shapes), mus=mus,
+        nesterovs=[nesterov] * len(shapes), device=torch.device(DEV), dtype=tdt,
+    )
+    return grp, grads, moms
+
+
+@pytest.mark.parametrize("name,shapes,th,tw,dtype,nesterov", GATHER_CASES, ids=[c[0] for c in GATHER_CASES])
+def test_gather_bit_exact(name, shapes, th, tw, dtype, nesterov):
+    print(f"[gather] {name}", flush=True)
+    mus = [0.95, 0.9, 0.8][: len(shapes)]
+    grp, grads, moms = _make_group(shapes, th, tw, dtype, nesterov, seed=10, mus=mus)
+    g_np = [g.float().cpu().numpy() for g in grads]
+    m_np = [m.float().cpu().numpy() for m in moms]
+    grp.gather()
+    torch.cuda.synchronize()
+    tiles = grp.tiles.float().cpu().numpy()
+    ofs = 0
+    for i, s in enumerate(shapes):
+        ge, nb = O.momentum(g_np[i], m_np[i], mus[i], nesterov, dtype)
+        assert np.array_equal(_bits(moms[i]), _bits(torch.from_numpy(nb).to(TDT[dtype]))), f"momentum param {i}"
+        exp = _ns_layout(O.tile(O.bf16_round(ge), th, tw), grp.mp, grp.np)
+        got = tiles[ofs : ofs + exp.shape[0]]
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), f"tiles param {i}"
+        ofs += exp.shape[0]
+    assert ofs == grp.n_tiles
+    # per-tile norm and normaliser
+    ssq = (tiles.astype(np.float64) ** 2).sum(axis=(1, 2))
+    np.testing.assert_allclose(grp.partials.double().sum(1).cpu().numpy(), ssq, rtol=1e-5, atol=1e-30)
+    inv = grp.inv.cpu().numpy()
+    np.testing.assert_allclose(inv, 1.0 / (np.sqrt(ssq) + 1e-7), rtol=1e-5)
+
+
+def test_gather_without_momentum_is_a_cast():
+    grp, grads, _ = _make_group([(300, 700)], 256, 256, "float32", True, seed=3, with_mom=False)
+    grp.gather()
+    exp = _ns_layout(O.tile(O.bf16_round(grads[0].cpu().numpy()), 256, 256), grp.mp, grp.np)
+    assert np.array_equal(grp.tiles.float().cpu().numpy(), exp)
+
+
+@pytest.mark.parametrize("name,shapes,th,tw,dtype,nesterov", GATHER_CASES, ids=[c[0] for c in GATHER_CASES])
+def test_untile_bit_exact(name, shapes, th, tw, dtype, nesterov):
+    print(f"[untile] {name}", flush=True)
+    grp, grads, _ = _make_group(shapes, th, tw, dtype, nesterov, seed=20)
+    gen = torch.Generator().manual_seed(5)
+    vals = torch.randn(grp.tiles.shape, generator=gen).to(torch.bfloat16)
+    grp.tiles.copy_(vals.to(DEV))
+    for u in grp.updates:
+        u.fill_(float("nan"))
+    grp.untile()
+    torch.cuda.synchronize()
+    v = vals.float().numpy()
+    ofs = 0
+    scale = np.float32(O.lr_scale((th, tw)))
+    for i, s in enumerate(shapes):
+        R, Cc = O.tile_grid(s[0], s[1], th, tw)
+        ns = v[ofs : ofs + R * Cc]
+        t = ns[:, : min(th, tw), : max(th, tw)]
+        t = np.swapaxes(t, 1, 2) if th > tw else t
+        exp = O.round_to(O.untile(np.ascontiguousarray(t), s[0], s[1]) * scale, dtype)
+        got = grp.updates[i].float().cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), f"param {i}"
+        ofs += R * Cc
+
+
+# ---------------------------------------------------------------------------
+# NS5
+# ---------------------------------------------------------------------------
+def _ns_engine(G: torch.Tensor, steps=5) -> torch.Tensor:
+    return newton_schulz(G, steps=steps)
+
+
+NS_SHAPES = [
+    # the reference's dispatch shapes (test_kernels.py:224-235)
+    ("square_128", (4, 128, 128)),
+    ("square_64", (8, 64, 64)),
+    ("wide_64x256", (4, 64, 256)),
+    ("tall_128x64", (4, 128, 64)),
+    ("big_512", (4, 512, 512)),
+    ("2d_square_512", (512, 512)),
+    ("2d_nondiv", (768, 513)),
+    ("2d_tall", (513, 768)),
+]
+
+
+@pytest.mark.parametrize("label,shape", NS_SHAPES, ids=[s[0] for s in NS_SHAPES])
+def test_newton_schulz_matches_reference_on_well_conditioned(label, shape):
+    """HiMuon.newton_schulz == the reference's NS in bf16 on well-conditioned
+    inputs, with the reference test's elementwise tolerance (4e-2) and the
+    north star's per-tile relative Frobenius bound (1e-2)."""
+    print(f"[ns5 wc] {label} {shape}", flush=True)
+    G = well_conditioned(shape, torch.bfloat16, seed=0)
+    out = _ns_engine(G)
+    assert out.shape == G.shape and out.dtype == G.dtype
+    assert torch.isfinite(out).all()
+    ref_eager = ns5_torch_eager(G)
+    assert torch.allclose(out.float(), ref_eager.float(), rtol=4e-2, atol=4e-2), label
+    ref = ns5_torch_staged(G)
+    err = per_tile_rel_fro(out, ref)
+    print(f"  rel-fro vs staged torch: max {err.max():.4f} mean {err.mean():.4f}", flush=True)
+    assert err.max() <= 1e-2, err
+
+
+@pytest.mark.parametrize("T,n", [(128, 32), (256, 16), (512, 8)])
+def test_ns5_random_tiles_vs_oracle_and_torch(T, n):
+    """Random (momentum-like) tiles: per-tile error against the torch
+    same-dtype NS5 and the CPU oracle, next to the distance between those two
+    references themselves (the summation-order noise floor of bf16 NS5)."""
+    print(f"[ns5 random] T={T} n={n}", flush=True)
+    G = _cpu_randn((n, T, T), seed=T, scale=1e-3).to(DEV)
+    out = _ns_engine(G)
+    ref_t = ns5_torch_staged(G)
+    ref_o = torch.from_numpy(O.ns5_staged(G.cpu().numpy())).to(DEV)
+    e_t = per_tile_rel_fro(out, ref_t)
+    e_o = per_tile_rel_fro(out, ref_o)
+    floor = per_tile_rel_fro(ref_t, ref_o)
+    print(f"  vs torch max {e_t.max():.4f} mean {e_t.mean():.4f} | vs oracle max {e_o.max():.4f} "
+          f"mean {e_o.mean():.4f} | torch vs oracle max {floor.max():.4f} mean {floor.mean():.4f}", flush=True)
+    assert e_t.mean() <= 1e-2 and e_o.mean() <= 1e-2
+    assert e_t.max() <= 2e-2 and e_o.max() <= 2e-2
+    # as close to each reference as the two references are to each other
+    assert e_t.mean() <= 1.5 * floor.mean() + 1e-3
+
+
+@pytest.mark.parametrize("T,n", [(128, 16), (512, 4)])
+def test_ns5_singular_value_band(T, n):
+    G = _cpu_randn((n, T, T), seed=T + 1, scale=1e-3).to(DEV)
+    out = _ns_engine(G).double()
+    sv = torch.linalg.svdvals(out).cpu().numpy()
+    ref_sv = torch.linalg.svdvals(ns5_torch_staged(G).double()).cpu().numpy()
+    sv_in = torch.linalg.svdvals(G.double()).cpu().numpy()
+    sv_in = sv_in / np.linalg.norm(G.double().cpu().numpy(), axis=(-2, -1))[:, None]
+    floor, tol = 4e-3, 0.03
+    for k in range(n):
+        lo, hi = O.quintic_band(max(sv_in[k].min(), floor), sv_in[k].max())
+        nn_ = int((sv_in[k] < floor).sum())
+        assert sv[k].max() <= hi + tol and ref_sv[k].max() <= hi + tol
+        assert (sv[k] < lo - tol).sum() <= nn_
+        # same band as the reference: extremes agree
+        assert abs(sv[k].max() - ref_sv[k].max()) < tol
+        assert abs(np.sort(sv[k])[nn_] - np.sort(ref_sv[k])[nn_]) < 0.05
+
+
+def test_ns5_zero_tile_and_padding():
+    # zero tiles map to zero (0 / (0 + eps) = 0); zero padding stays zero and
+    # does not change the data block (a 37x100 block in a 256x256 tile equals
+    # the same block NS'd in its own 128x128 padding, bit for bit)
+    G = torch.zeros(3, 256, 256, device=DEV)
+    G[1, :37, :100] = _cpu_randn((37, 100), 4).to(DEV)
+    out = _ns_engine(G)
+    assert (out[0] == 0).all() and (out[2] == 0).all()
+    assert (out[1, 37:] == 0).all() and (out[1, :, 100:] == 0).all()
+    small = _ns_engine(G[1:2, :37, :100].contiguous())
+    assert torch.equal(out[1, :37, :100], small[0])
+
+
+@pytest.mark.parametrize("steps", [0, 1, 2, 5])
+def test_ns5_steps_honoured(steps):
+    G = _cpu_randn((2, 128, 256), seed=9).to(DEV)
+    out = _ns_engine(G, steps=steps)
+    ref = torch.from_numpy(O.ns5_staged(G.cpu().numpy(), steps=steps)).to(DEV)
+    assert per_tile_rel_fro(out, ref).max() <= 1.5e-2
+
+
+def test_ns5_sub_batch_invariance():
+    """Sub-batching (tiles are independent) does not change results bitwise."""
+    G = _cpu_randn((10, 256, 256), seed=12, scale=1e-3).to(DEV)
+    grp = TileGroup([G.view(-1, 256)], [G.view(-1, 256)], [None], 256, 256, [1.0], [0.0], [False],
+                    torch.device(DEV), torch.float32)
+    grp.gather()
+    base = grp.tiles.clone()
+    outs = []
+    for sb in (1, 3, 10):
+        grp.tiles.copy_(base)
+        ws = torch.empty(grp.workspace_bytes(sb), device=DEV, dtype=torch.uint8)
+        grp.ns(0, grp.n_tiles, 5, ws, sb)
+        outs.append(grp.tiles.clone())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+def test_ns5_workspace_too_small_raises():
+    G = _cpu_randn((2, 128, 128), seed=1).to(DEV)
+    grp = TileGroup([G.view(-1, 128)], [G.view(-1, 128)], [None], 128, 128, [1.0], [0.0], [False],
+                    torch.device(DEV), torch.float32)
+    grp.gather()
+    ws = torch.empty(16, device=DEV, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="workspace"):
+        grp.ns(0, 2, 5, ws, 2)

@@ -1,0 +1,317 @@
+"""GPU behaviour of HiMuon.step() on the HIP path.
+
+Step-level parity against the CPU oracle (oracle.step_param), bit-exact
+momentum buffers, self-consistency (b_hw chunking, eager vs hipGraph replay,
+reconfigure to the same tile), plan/dispatch accounting, cache invalidation,
+peak-memory stability and a smoke matrix — the behaviours the reference pins
+in tests/integration/test_himuon_{self_consistency,dispatch,reconfigure,
+memory,smoke}.py.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import himuon_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from himuon_amd.optimizers.himuon import HiMuon
+
+DEV = "cuda"
+RTOL = ATOL = 1e-2  # reference self-consistency tolerance (test_himuon_self_consistency.py:18)
+
+
+def make_model(shapes, dtype=torch.float32, bias=False, seed=0):
+    torch.manual_seed(seed)
+    layers = [nn.Linear(w, h, bias=bias, dtype=dtype) for (h, w) in shapes]
+    return nn.ModuleList(layers).to(DEV)
+
+
+def muon_groups(model, wd=0.0, **extra):
+    muon = [p for p in model.parameters() if p.ndim >= 2]
+    one_d = [p for p in model.parameters() if p.ndim < 2]
+    groups = [{"params": muon, "weight_decay": wd, "use_muon": True, **extra}]
+    if one_d:
+        groups.append({"params": one_d, "lr": 1e-3, "weight_decay": 0.0, "use_muon": False})
+    return groups
+
+
+def seed_grads(model, seed):
+    """Fill grads in place (stable pointers), from a CPU generator."""
+    g = torch.Generator().manual_seed(seed)
+    for p in model.parameters():
+        vals = torch.randn(p.shape, generator=g).to(p.dtype)
+        if p.grad is None:
+            p.grad = torch.empty_like(p)
+        p.grad.copy_(vals.to(DEV))
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+# ---------------------------------------------------------------------------
+# Parity against the oracle
+# ---------------------------------------------------------------------------
+STEP_CASES = [
+    ("fp32_T256", [(512, 1024), (256, 512), (1024, 2048)], 256, torch.float32),
+    ("bf16_T512_pad", [(768, 513), (512, 1024)], 512, torch.bfloat16),
+    ("fp32_tall_tiles", [(384, 256)], (128, 64), torch.float32),
+    ("full_ns_mix", [(64, 64), (256, 1024), (100, 40)], 512, torch.float32),
+]
+
+
+@pytest.mark.parametrize("name,shapes,tile,dtype", STEP_CASES, ids=[c[0] for c in STEP_CASES])
+def test_step_matches_oracle(name, shapes, tile, dtype):
+    print(f"[step vs oracle] {name}", flush=True)
+    lr, wd, steps = 0.02, 0.1, 3
+    model = make_model(shapes, dtype)
+    opt = HiMuon(muon_groups(model, wd=wd), lr=lr, tile_size=tile, cuda_graph=False)
+    ts = opt.param_groups[0]["tile_size"]
+    p_np = [_np(p) for p in model.parameters()]
+    bufs = [None] * len(p_np)
+    dname = "bfloat16" if dtype == torch.bfloat16 else "float32"
+    for k in range(steps):
+        seed_grads(model, 100 + k)
+        g_np = [_np(p.grad) for p in model.parameters()]
+        opt.step()
+        for i in range(len(p_np)):
+            op = O.OracleParam(p=p_np[i], g=g_np[i], buf=bufs[i], tile=ts, lr=lr, wd=wd,
+                               p_dtype=dname, g_dtype=dname)
+            p_np[i], bufs[i], _ = O.step_param(op)
+    for i, p in enumerate(model.parameters()):
+        buf = opt.state[p]["momentum_buffer"]
+        assert np.array_equal(_np(buf), bufs[i]), f"momentum buffer {i} not bit-exact"
+        np.testing.assert_allclose(_np(p), p_np[i], rtol=RTOL, atol=ATOL)
+        # the update itself: relative to the total update size
+        upd_ref = p_np[i]
+        assert np.isfinite(_np(p)).all()
+
+
+def test_update_tensor_matches_oracle_per_tile():
+    """One step; the update tensor of each param vs the oracle's, per tile
+    (relative Frobenius), bit-exact momentum."""
+    shapes, T = [(1024, 1536)], 512
+    model = make_model(shapes, torch.float32)
+    opt = HiMuon(muon_groups(model), tile_size=T, cuda_graph=True, cuda_graph_warmup=0)
+    seed_grads(model, 7)
+    g = _np(model[0].weight.grad)
+    opt.step()  # capture + replay
+    upd = [u for (_, u, _) in opt._pending_updates][0]
+    ge, _ = O.momentum(g, np.zeros_like(g), 0.95, True)
+    ref = O.untile(O.ns5_staged(O.tile(ge, T, T)), *shapes[0]) * np.float32(O.lr_scale((T, T)))
+    got = _np(upd)
+    for r in range(2):
+        for c in range(3):
+            sl = (slice(r * T, (r + 1) * T), slice(c * T, (c + 1) * T))
+            e = np.linalg.norm(got[sl] - ref[sl]) / np.linalg.norm(ref[sl])
+            assert e < 2e-2, (r, c, e)
+
+
+# ---------------------------------------------------------------------------
+# Self-consistency (test_himuon_self_consistency.py)
+# ---------------------------------------------------------------------------
+SHAPES = [(512, 1024), (256, 512), (1024, 2048)]
+
+
+def test_result_invariant_to_b_hw():
+    kw = dict(lr=0.02, weight_decay=0.1, tile_size=512, ns_steps=5, cuda_graph=False)
+    m_big = make_model(SHAPES, torch.bfloat16)
+    m_small = copy.deepcopy(m_big)
+    o_big = HiMuon(muon_groups(m_big, wd=0.1), b_hw=100_000, **kw)
+    o_small = HiMuon(muon_groups(m_small, wd=0.1), b_hw=1, **kw)
+    for k in range(5):
+        seed_grads(m_big, 100 + k)
+        seed_grads(m_small, 100 + k)
+        o_big.step()
+        o_small.step()
+    for a, b in zip(m_big.parameters(), m_small.parameters()):
+        assert torch.equal(a, b)  # tiles are independent: chunking is exact
+
+
+def test_eager_matches_graph():
+    kw = dict(lr=0.02, weight_decay=0.05, tile_size=512, ns_steps=5)
+    m_e = make_model(SHAPES, torch.bfloat16)
+    m_g = copy.deepcopy(m_e)
+    o_e = HiMuon(muon_groups(m_e, wd=0.05), cuda_graph=False, **kw)
+    o_g = HiMuon(muon_groups(m_g, wd=0.05), cuda_graph=True, cuda_graph_warmup=3, **kw)
+    for k in range(8):
+        seed_grads(m_e, 200 + k)
+        seed_grads(m_g, 200 + k)
+        o_e.step()
+        o_g.step()
+    assert o_g._cuda_graph is not None
+    for a, b in zip(m_e.parameters(), m_g.parameters()):
+        assert torch.equal(a, b)
+
+
+def test_graph_replays_track_lr_schedule():
+    """LR/WD are read outside the graph: changing group lr between replays
+    takes effect without recapture."""
+    m_e = make_model([(512, 1024)], torch.float32)
+    m_g = copy.deepcopy(m_e)
+    o_e = HiMuon(muon_groups(m_e, wd=0.1), tile_size=256, cuda_graph=False)
+    o_g = HiMuon(muon_groups(m_g, wd=0.1), tile_size=256, cuda_graph=True, cuda_graph_warmup=1)
+    for k in range(6):
+        for o in (o_e, o_g):
+            o.param_groups[0]["lr"] = 0.02 * (k + 1) / 6
+        seed_grads(m_e, 300 + k)
+        seed_grads(m_g, 300 + k)
+        o_e.step()
+        o_g.step()
+    for a, b in zip(m_e.parameters(), m_g.parameters()):
+        assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# Dispatch / plan (test_himuon_dispatch.py)
+# ---------------------------------------------------------------------------
+MULTI = [(512, 1024), (256, 512), (1024, 2048)]
+
+
+def test_every_tile_accounted_for():
+    T = 256
+    model = make_model(MULTI, bias=True)
+    opt = HiMuon(muon_groups(model), tile_size=T, cuda_graph=False)
+    seed_grads(model, 12)
+    opt.step()
+    counts = {}
+    for b in opt.xlayer_plan():
+        for pid, tc in zip(b["param_ids"], b["tile_count_per_param"]):
+            counts[pid] = counts.get(pid, 0) + tc
+    for p in model.parameters():
+        if p.ndim < 2:
+            continue
+        exp = (-(-p.shape[0] // T)) * (-(-p.shape[1] // T))
+        if id(p) in counts:
+            assert counts[id(p)] == exp
+        else:
+            assert p.numel() <= T * T
+    assert opt._last_step_stats["ns_launches"] >= 1
+
+
+def test_chunks_and_override():
+    model = make_model(MULTI)
+    opt = HiMuon(muon_groups(model), tile_size=512, cuda_graph=False)
+    seed_grads(model, 14)
+    opt.step()
+    for b in opt.xlayer_plan():
+        assert sum(b["chunk_sizes"]) == b["B_total"] and all(0 < c <= b["B_hw"] for c in b["chunk_sizes"])
+        assert b["n_calls"] == len(b["chunk_sizes"])
+    B_total = max(b["B_total"] for b in opt.xlayer_plan())
+    for b_hw, n_expect in ((B_total + 10, 1), (B_total, 1), (max(1, B_total // 2), -(-B_total // max(1, B_total // 2)))):
+        m = make_model(MULTI)
+        o = HiMuon(muon_groups(m), tile_size=512, b_hw=b_hw, cuda_graph=False)
+        seed_grads(m, 19)
+        o.step()
+        assert o.xlayer_plan()[0]["n_calls"] == n_expect
+    m = make_model([(1024, 1024)])
+    o = HiMuon(muon_groups(m), tile_size=512, b_hw=7, cuda_graph=False)
+    seed_grads(m, 22)
+    o.step()
+    assert o.xlayer_plan()[0]["B_hw"] == 7
+
+
+# ---------------------------------------------------------------------------
+# Reconfigure (test_himuon_reconfigure.py)
+# ---------------------------------------------------------------------------
+def test_reconfigure_invalidates_and_takes_effect():
+    model = make_model([(512, 1024)], torch.bfloat16)
+    opt = HiMuon(muon_groups(model), tile_size=512, cuda_graph=True, cuda_graph_warmup=2)
+    for k in range(4):
+        seed_grads(model, 10 + k)
+        opt.step()
+    assert opt._cuda_graph is not None and opt._pending_updates and opt.xlayer_plan() and opt._concat_buffers
+    opt.reconfigure(tile_size=256)
+    assert opt._cuda_graph is None and opt._graph_step_count == 0 and opt._pending_updates == []
+    assert opt.xlayer_plan() == [] and opt._concat_buffers == {}
+    seed_grads(model, 20)
+    opt.step()
+    assert {(b["bucket_key"][0], b["bucket_key"][1]) for b in opt.xlayer_plan()} == {(256, 256)}
+
+
+@pytest.mark.parametrize("cuda_graph", [False, True])
+def test_reconfigure_same_tile_is_noop(cuda_graph):
+    shapes, K = [(512, 1024), (256, 512)], 6
+    ref = make_model(shapes, torch.bfloat16)
+    rec = copy.deepcopy(ref)
+    kw = dict(lr=0.02, weight_decay=0.05, tile_size=256, cuda_graph=cuda_graph, cuda_graph_warmup=2)
+    o_ref = HiMuon(muon_groups(ref, wd=0.05), **kw)
+    o_rec = HiMuon(muon_groups(rec, wd=0.05), **kw)
+    for k in range(2 * K):
+        seed_grads(ref, 200 + k)
+        seed_grads(rec, 200 + k)
+        o_ref.step()
+        if k == K:
+            o_rec.reconfigure(tile_size=256)
+        o_rec.step()
+    for a, b in zip(ref.parameters(), rec.parameters()):
+        assert torch.equal(a, b)
+
+
+def test_reconfigure_128_to_512_recaptures():
+    """Small-tile regime then a mid-run reconfigure to 512 (graph recapture)."""
+    model = make_model([(1024, 1024), (512, 2048)], torch.float32)
+    opt = HiMuon(muon_groups(model, wd=0.1), tile_size=128, cuda_graph=True, cuda_graph_warmup=1)
+    for k in range(3):
+        seed_grads(model, k)
+        opt.step()
+    assert opt.xlayer_plan()[0]["B_total"] == 64 + 64
+    g1 = opt._cuda_graph
+    opt.reconfigure(tile_size=512)
+    for k in range(3):
+        seed_grads(model, 10 + k)
+        opt.step()
+    assert opt._cuda_graph is not None and opt._cuda_graph is not g1
+    assert opt.xlayer_plan()[0]["B_total"] == 4 + 4
+    assert all(torch.isfinite(p).all() for p in model.parameters())
+
+
+# ---------------------------------------------------------------------------
+# Memory (test_himuon_memory.py) and smoke (test_himuon_smoke.py)
+# ---------------------------------------------------------------------------
+def test_no_peak_memory_growth():
+    model = make_model([(1024, 1024), (512, 2048)])
+    opt = HiMuon(muon_groups(model, wd=0.1), tile_size=512)
+    for i in range(8):
+        seed_grads(model, 300 + i)
+        opt.step()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    peaks = []
+    for i in range(10):
+        torch.cuda.reset_peak_memory_stats()
+        seed_grads(model, 400 + i)
+        opt.step()
+        torch.cuda.synchronize()
+        peaks.append(torch.cuda.max_memory_allocated())
+    assert (max(peaks) - min(peaks)) / max(min(peaks), 1) < 0.01, peaks
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("tile", [128, 256, 512])
+def test_smoke_finite_and_changed(dtype, tile):
+    model = make_model([(512, 1024), (768, 513), (64, 64)], dtype, bias=True)
+    opt = HiMuon(muon_groups(model), tile_size=tile, cuda_graph=False)
+    before = [p.detach().clone() for p in model.parameters()]
+    seed_grads(model, 1)
+    opt.step()
+    assert all(torch.isfinite(p).all() for p in model.parameters())
+    assert any(not torch.equal(p, b) for p, b in zip(model.parameters(), before))
+
+
+def test_closure_and_cuda_graph_mode_runs():
+    model = make_model([(512, 1024)])
+    opt = HiMuon(muon_groups(model), tile_size=512, cuda_graph=True, cuda_graph_warmup=2)
+    for k in range(5):
+        seed_grads(model, 20 + k)
+        assert opt.step(closure=lambda: 1.5) == 1.5
+    assert opt._cuda_graph is not None
+    assert all(torch.isfinite(p).all() for p in model.parameters())

@@ -1,0 +1,342 @@
+"""Pin the CPU oracle (oracle/himuon_oracle.py) before it is trusted.
+
+Each oracle function is checked against something that does not share its
+code: torch's own ops, brute-force loops, committed fixtures
+(tests/golden/golden.npz, made by tests/golden/make_golden.py), closed forms
+of the quintic map (SVD, rank-1, diagonal), invariances, and planted mistakes
+that the checks must catch.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import himuon_oracle as O
+
+GOLDEN = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
+
+
+def _rel_fro(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
+
+
+# ---------------------------------------------------------------------------
+# bf16 rounding
+# ---------------------------------------------------------------------------
+def test_bf16_round_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    x = np.concatenate(
+        [
+            (rng.standard_normal(20000) * 10.0 ** rng.integers(-30, 30, 20000)).astype(np.float32),
+            # exact ties between two bf16 values (low 16 bits = 0x8000)
+            (rng.integers(0, 0x7F00, 2000, dtype=np.uint32) << 16 | 0x8000).view(np.float32),
+            -(rng.integers(0, 0x7F00, 2000, dtype=np.uint32) << 16 | 0x8000).view(np.float32),
+            np.array([0.0, -0.0, np.inf, -np.inf, 3.4e38, -3.4e38, 1e-45, -1e-40], dtype=np.float32),
+        ]
+    ).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    got = O.bf16_round(x)
+    fin = np.isfinite(ref)
+    assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+    assert np.array_equal(np.isinf(got), np.isinf(ref))
+    assert np.isnan(O.bf16_round(np.array([np.nan], np.float32))).all()
+
+
+# ---------------------------------------------------------------------------
+# Momentum (himuon.py:350-357)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_momentum_matches_torch_inplace_ops(dtype):
+    g = GOLDEN[f"mom_{dtype}_g"]
+    b0 = GOLDEN[f"mom_{dtype}_buf0"]
+    ge, b1 = O.momentum(g, b0, 0.95, True, dtype)
+    # buf.mul_(mu).add_(g): two stores, bit-exact
+    assert np.array_equal(b1.view(np.uint32), GOLDEN[f"mom_{dtype}_buf1"].view(np.uint32))
+    # g.add(buf, alpha=mu): one fused multiply-add, stored once — bit-exact.
+    ref = GOLDEN[f"mom_{dtype}_geff"]
+    if dtype == "float32":
+        assert np.array_equal(ge.view(np.uint32), ref.view(np.uint32))
+    else:
+        # torch's CPU kernel (which made the fixture) casts alpha to bf16
+        # before the fused multiply-add; the GPU kernel keeps alpha in fp32
+        # (opmath), which is what the oracle and the HIP kernel do. Pin the
+        # fma-then-round structure with the CPU's alpha.
+        alpha_bf16 = O.bf16_round(np.float32(0.95))
+        cpu_form = O.bf16_round(O.fma32(alpha_bf16, b1, g))
+        assert np.array_equal(cpu_form.view(np.uint32), ref.view(np.uint32))
+        assert np.array_equal(ge.view(np.uint32), O.bf16_round(O.fma32(np.float32(0.95), b1, g)).view(np.uint32))
+
+
+def test_fma32_is_correctly_rounded():
+    """fma32 against exact rational arithmetic, including cancellation and
+    halfway cases that a float64 evaluation would double-round."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal(3000).astype(np.float32)
+    b = rng.standard_normal(3000).astype(np.float32)
+    c = (-(a.astype(np.float64) * b) * (1 + rng.standard_normal(3000) * 1e-7)).astype(np.float32)
+    # halfway constructions: a*b = 1 + 2^-24 (a tie in fp32) plus tiny c
+    a = np.concatenate([a, np.float32([1 + 2**-12, 1 + 2**-12, 1 + 2**-23])])
+    b = np.concatenate([b, np.float32([1 + 2**-12, 1 + 2**-12, 1 - 2**-23])])
+    c = np.concatenate([c, np.float32([2**-60, -(2**-60), 0.0])])
+    got = O.fma32(a, b, c)
+    for x, y, z, r in zip(a, b, c, got):
+        exact = Fraction(float(x)) * Fraction(float(y)) + Fraction(float(z))
+        lo = np.float32(float(exact))
+        # the correctly rounded fp32 value is the nearest of lo's neighbours
+        cands = [np.nextafter(lo, np.float32(-np.inf)), lo, np.nextafter(lo, np.float32(np.inf))]
+        best = min(cands, key=lambda v: (abs(Fraction(float(v)) - exact), int(np.float32(v).view(np.uint32)) & 1))
+        assert r == best, (x, y, z, r, best)
+
+
+def test_momentum_plain_and_closed_form():
+    rng = np.random.default_rng(1)
+    g = rng.standard_normal((8, 8)).astype(np.float32)
+    b = rng.standard_normal((8, 8)).astype(np.float32)
+    ge, nb = O.momentum(g, b, 0.9, False)
+    assert np.array_equal(ge, nb)
+    np.testing.assert_allclose(nb, 0.9 * b.astype(np.float64) + g, rtol=1e-6)
+    ge2, _ = O.momentum(g, b, 0.9, True)
+    np.testing.assert_allclose(ge2, g + 0.9 * (0.9 * b.astype(np.float64) + g), rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Tiling (himuon.py:288-310, 704-719)
+# ---------------------------------------------------------------------------
+def _brute_tile_map(h, w, th, tw):
+    R, C = -(-h // th), -(-w // tw)
+    out = np.full((R * C, th, tw), -1, dtype=np.int64)
+    for t in range(R * C):
+        r, c = divmod(t, C)
+        for i in range(th):
+            for j in range(tw):
+                row, col = r * th + i, c * tw + j
+                if row < h and col < w:
+                    out[t, i, j] = row * w + col
+    return out
+
+
+@pytest.mark.parametrize("k", range(5))
+def test_tile_map_golden(k):
+    h, w, th, tw = (int(v) for v in GOLDEN[f"tilemap_{k}_args"])
+    assert np.array_equal(O.tile_source_map(h, w, th, tw), GOLDEN[f"tilemap_{k}"])
+
+
+@pytest.mark.parametrize("h,w,th,tw", [(768, 513, 512, 512), (1024, 1024, 256, 256), (100, 300, 64, 32), (5, 5, 8, 8)])
+def test_tile_untile_against_bruteforce(h, w, th, tw):
+    rng = np.random.default_rng(h * w)
+    x = rng.standard_normal((h, w)).astype(np.float32)
+    m = _brute_tile_map(h, w, th, tw) if h * w <= 100_000 else O.tile_source_map(h, w, th, tw)
+    if h * w <= 100_000:
+        assert np.array_equal(O.tile_source_map(h, w, th, tw), m)
+    t = O.tile(x, th, tw)
+    flat = x.reshape(-1)
+    expect = np.where(m >= 0, flat[np.clip(m, 0, None)], 0.0)
+    assert np.array_equal(t, expect)
+    assert np.array_equal(O.untile(t, h, w), x)
+    # every element lands in exactly one tile slot
+    assert np.array_equal(np.sort(m[m >= 0]), np.arange(h * w))
+
+
+def test_tile_grid_counts_match_reference_accounting():
+    # tests/integration/test_himuon_dispatch.py:105-112: R = ceil(H/T), C = ceil(W/T)
+    for h, w, t in [(512, 1024, 256), (256, 512, 256), (1024, 2048, 512), (768, 513, 512)]:
+        assert O.tile_grid(h, w, t, t) == (-(-h // t), -(-w // t))
+
+
+# ---------------------------------------------------------------------------
+# Plan (himuon.py:376-403, 459-586)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B,b", [(1, 1), (16, 3), (1680, 11059), (13860, 11059), (425984, 176947), (7, 7), (100, 33)])
+def test_balanced_chunks_invariants(B, b):
+    ch = O.balanced_chunks(B, b)
+    assert sum(ch) == B
+    assert len(ch) == -(-B // b)
+    assert all(0 < c <= b for c in ch)
+    assert max(ch) - min(ch) <= 1
+    assert ch == sorted(ch, reverse=True)
+
+
+def test_plan_worked_values():
+    gib288 = 288 * 2**30
+    assert O.auto_b_hw(512, 4, gib288) == 11059
+    assert O.balanced_chunks(13860, 11059) == [6930, 6930]
+    assert O.auto_b_hw(512, 4, None) == 1 and O.auto_b_hw(512, 4, None, override=5) == 5
+    assert O.auto_b_hw(512, 4, gib288, override=7) == 7
+    # Qwen3-4B set: 385 tiles per layer at T=512
+    shapes = [(4096, 2560), (1024, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (9728, 2560), (2560, 9728)]
+    assert sum(O.tile_grid(h, w, 512, 512)[0] * O.tile_grid(h, w, 512, 512)[1] for h, w in shapes) == 385
+    plan = O.plan_buckets([O.PlanParam(s, (512, 512)) for s in shapes * 36], gib288)
+    assert len(plan) == 1 and plan[0]["B_total"] == 13860 and plan[0]["chunk_sizes"] == [6930, 6930]
+    # numel <= tile area -> full-NS path, not in the plan
+    plan = O.plan_buckets([O.PlanParam((64, 64), (128, 128)), O.PlanParam((512, 1024), (512, 512))], gib288)
+    assert plan[0]["params"] == [1]
+
+
+# ---------------------------------------------------------------------------
+# Newton-Schulz
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("k", range(4))
+def test_ns5_fp64_matches_golden_svd(k):
+    G = GOLDEN[f"ns_{k}_in"]
+    assert _rel_fro(O.ns5_fp64(G), GOLDEN[f"ns_{k}_out"]) < 1e-9
+    assert _rel_fro(O.ns5_spectral(G), GOLDEN[f"ns_{k}_out"]) < 1e-9
+
+
+@pytest.mark.parametrize("shape", [(4, 16, 16), (3, 12, 40), (2, 40, 12), (24, 7)])
+def test_ns5_fp64_matches_spectral_closed_form(shape):
+    G = np.random.default_rng(sum(shape)).standard_normal(shape)
+    assert _rel_fro(O.ns5_fp64(G), O.ns5_spectral(G)) < 1e-9
+
+
+def test_ns5_rank1_closed_form():
+    rng = np.random.default_rng(3)
+    u = rng.standard_normal(12); u /= np.linalg.norm(u)
+    v = rng.standard_normal(20); v /= np.linalg.norm(v)
+    s = 3.7
+    out = O.ns5_fp64(s * np.outer(u, v))
+    expect = O.quintic(s / (s + O.NS_EPS)) * np.outer(u, v)
+    assert _rel_fro(out, expect) < 1e-12
+
+
+@pytest.mark.parametrize("m,n", [(6, 6), (5, 9), (9, 5)])
+def test_ns5_diagonal_closed_form(m, n):
+    d = np.array([2.0, 1.0, 0.5, 0.25, 0.1][: min(m, n)] + [0.3] * max(0, min(m, n) - 5))
+    G = np.zeros((m, n))
+    G[np.arange(len(d)), np.arange(len(d))] = d
+    out = O.ns5_fp64(G)
+    expect = np.zeros((m, n))
+    expect[np.arange(len(d)), np.arange(len(d))] = O.quintic(d / (np.linalg.norm(d) + O.NS_EPS))
+    assert np.abs(out - expect).max() < 1e-12
+
+
+def test_ns5_invariances():
+    rng = np.random.default_rng(5)
+    G = rng.standard_normal((10, 14))
+    Q1 = np.linalg.qr(rng.standard_normal((10, 10)))[0]
+    Q2 = np.linalg.qr(rng.standard_normal((14, 14)))[0]
+    assert _rel_fro(O.ns5_fp64(Q1 @ G @ Q2), Q1 @ O.ns5_fp64(G) @ Q2) < 1e-10
+    assert _rel_fro(O.ns5_fp64(G.T), O.ns5_fp64(G).T) < 1e-12
+    assert np.array_equal(O.ns5_fp64(np.zeros((4, 6))), np.zeros((4, 6)))
+    # zero padding is exact
+    P = np.zeros((16, 20)); P[:10, :14] = G
+    out = O.ns5_fp64(P)
+    assert _rel_fro(out[:10, :14], O.ns5_fp64(G)) < 1e-12 and np.abs(out[10:]).max() == 0 and np.abs(out[:, 14:]).max() == 0
+
+
+def test_quintic_band():
+    s = np.geomspace(0.01, 1.0, 20001)
+    f = O.quintic(s)
+    assert 0.68 < f.min() and f.max() < 1.135
+    f3 = O.quintic(np.geomspace(1e-3, 1.0, 20001))
+    assert 0.47 < f3.min() and f3.max() < 1.21
+
+
+def _planted_variants():
+    a, b, c = O.NS_A, O.NS_B, O.NS_C
+
+    def wrong_gram(G):  # X^T X instead of X X^T (square only would pass silently)
+        X = np.asarray(G, float) / (np.linalg.norm(G) + O.NS_EPS)
+        for _ in range(5):
+            A = X.T @ X
+            X = a * X + X @ (b * A + c * A @ A) if False else a * X + (b * A + c * A @ A)[: X.shape[0], : X.shape[0]] @ X
+        return X
+
+    def dropped_ax(G):
+        X = np.asarray(G, float) / (np.linalg.norm(G) + O.NS_EPS)
+        for _ in range(5):
+            A = X @ X.T
+            X = (b * A + c * A @ A) @ X
+        return X
+
+    return {
+        "swapped_bc": lambda G: O.ns5_fp64(G, coeffs=(a, c, b)),
+        "sign_b": lambda G: O.ns5_fp64(G, coeffs=(a, -b, c)),
+        "four_steps": lambda G: O.ns5_fp64(G, steps=4),
+        "wrong_gram": wrong_gram,
+        "dropped_ax": dropped_ax,
+    }
+
+
+@pytest.mark.parametrize("name", list(_planted_variants()))
+def test_pins_catch_planted_mistakes(name):
+    """A plausible mistake in the NS oracle fails the closed-form check."""
+    fn = _planted_variants()[name]
+    G = np.random.default_rng(11).standard_normal((6, 9))
+    try:
+        with np.errstate(all="ignore"):
+            bad = fn(G)
+    except ValueError:
+        return  # shape error: caught
+    assert not (_rel_fro(bad, O.ns5_spectral(G)) <= 1e-3)
+
+
+def _well_conditioned(shape, seed):
+    """Spectrum in [0.8, 1.2] (test_kernels.py:201-215)."""
+    rng = np.random.default_rng(seed)
+    A = rng.standard_normal(shape)
+    U, _, Vt = np.linalg.svd(A, full_matrices=False)
+    k = U.shape[-1]
+    return (U * np.linspace(0.8, 1.2, k)) @ Vt
+
+
+@pytest.mark.parametrize("shape", [(4, 64, 64), (2, 32, 96), (2, 96, 32), (128, 128)])
+def test_staged_and_eager_within_bf16_of_exact(shape):
+    # bf16 staging through 5 chaotic iterations costs a few percent against
+    # exact arithmetic (measured: staged 1.5-2.6 %, eager 2.6-5.1 %); a wrong
+    # term or operand costs O(1).
+    G = _well_conditioned(shape, 2).astype(np.float32)
+    exact = O.ns5_fp64(G)
+    for fn, tol in ((O.ns5_staged, 3e-2), (O.ns5_eager, 6e-2)):
+        out = fn(G)
+        assert out.shape == G.shape
+        assert _rel_fro(out, exact) < tol, fn.__name__
+    assert _rel_fro(O.ns5_staged(G), O.ns5_eager(G)) < 6e-2
+
+
+def test_staged_singular_values_in_band():
+    """Output singular values lie in the quintic's band over the tile's
+    normalised input spectrum, and match quintic(sigma_in) one by one."""
+    G = np.random.default_rng(9).standard_normal((8, 64, 64)).astype(np.float32)
+    sv_in = np.linalg.svd(G.astype(np.float64), compute_uv=False)
+    sv_in = sv_in / np.linalg.norm(G.astype(np.float64), axis=(-2, -1))[:, None]
+    sv = np.linalg.svd(O.ns5_staged(G).astype(np.float64), compute_uv=False)
+    # bf16 staging adds noise of ~2^-8 of the largest sigma, so normalised
+    # inputs below ``floor`` carry no information; only they may leave the band.
+    tol, floor = 0.03, 4e-3
+    for k in range(G.shape[0]):
+        lo, hi = O.quintic_band(max(sv_in[k].min(), floor), sv_in[k].max())
+        n_noise = int((sv_in[k] < floor).sum())
+        assert sv[k].max() <= hi + tol
+        assert (sv[k] < lo - tol).sum() <= n_noise
+        big = np.sort(sv[k])[n_noise:]
+        assert np.abs(big - np.sort(O.quintic(sv_in[k]))[n_noise:]).max() < 0.1
+    assert O.quintic_band(0.01) == pytest.approx((0.6818, 1.1344), abs=2e-4)
+
+
+def test_staged_rounding_points():
+    """Every stored intermediate of ns5_staged is a bf16 value; zero stays zero."""
+    G = np.random.default_rng(4).standard_normal((3, 16, 24)).astype(np.float32)
+    out = O.ns5_staged(G)
+    assert np.array_equal(O.bf16_round(out), out)
+    assert np.array_equal(O.ns5_staged(np.zeros((2, 8, 8), np.float32)), np.zeros((2, 8, 8), np.float32))
+
+
+def test_step_param_composes_reference_formula():
+    rng = np.random.default_rng(8)
+    p = (rng.standard_normal((96, 160)) * 0.02).astype(np.float32)
+    g = (rng.standard_normal((96, 160)) * 1e-3).astype(np.float32)
+    op = O.OracleParam(p=p, g=g, buf=None, tile=(64, 64), lr=1e-2, wd=0.1)
+    newp, nb, upd = O.step_param(op)
+    ge = g + 0.95 * g  # first step: buf = g, nesterov
+    u = O.untile(O.ns5_fp64(O.tile(ge, 64, 64)), 96, 160)
+    expect = p * (1 - 1e-3) - 1e-2 * 0.2 * 8.0 * u
+    assert _rel_fro(newp - p * (1 - 1e-3), expect - p * (1 - 1e-3)) < 3e-2
+    assert np.array_equal(nb, g)
