@@ -33,6 +33,17 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 4096 FLOP/clk x 2.4 GHz)
+
+# NS stage kernels per kernel family (HIMUON_NS_PATH), per NS iteration.
+NS_KERNELS = {
+    "big": "ns5 stage: ns_gram256_kernel x2 + ns_apply256_kernel per iteration",
+    "nt": "ns5 stage: ns_nt_kernel (gram A, gram B, apply) per iteration",
+    "small": "ns5 stage: ns_gram_kernel x2 + ns_apply_kernel per iteration",
+}
+
+
+def ns_path() -> str:
+    return os.environ.get("HIMUON_NS_PATH", "big")
 PEAK_HBM_GBS = 8000.0
 
 CONFIGS = {
@@ -260,7 +271,7 @@ def main():
         "untile_ms": round(untile_ms, 3),
         "untile_gbs": round(6.0 * n_el / (untile_ms * 1e-3) / 1e9, 1),
         "roofline": {
-            "kernel": "ns5 stage (ns_gram_kernel x2 + ns_apply_kernel per iteration)",
+            "kernel": NS_KERNELS.get(ns_path(), ns_path()),
             "bound": "mfma",
             "achieved": round(ns_tflops, 1),
             "peak": PEAK_BF16_TFLOPS,

@@ -59,13 +59,16 @@ _SIGNATURES = {
     "himuon_gather_partials_per_tile": (c_int, [c_int, c_int, c_int, c_int]),
     "himuon_momentum_gather": (
         c_int,
-        [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p],
+        [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
+         c_void_p],
     ),
     "himuon_tile_scale": (c_int, [c_void_p, c_int, c_int64, c_float, c_void_p, c_void_p]),
     "himuon_ns5_workspace_bytes": (c_size_t, [c_int64, c_int, c_int]),
     "himuon_ns5": (
         c_int,
         [
+            c_void_p,
+            c_void_p,
             c_void_p,
             c_void_p,
             c_void_p,
@@ -168,13 +171,28 @@ def ns5_workspace_bytes(sub_batch: int, mp: int, np_: int) -> int:
     return int(load().himuon_ns5_workspace_bytes(sub_batch, mp, np_))
 
 
+def ns_path() -> str:
+    """NS kernel family: HIMUON_NS_PATH = "big" (256-blocks, the default for
+    256-aligned tiles), "nt" (persistent 256-block kernel reading X and X^T)
+    or "small" (128-blocks for every shape)."""
+    return os.environ.get("HIMUON_NS_PATH", "big")
+
+
+def nt_path(mp: int, np_: int) -> bool:
+    """True when the NS stage runs the persistent NT kernel, which also needs
+    the transposed X buffers: both padded edges multiples of 256 and the
+    "nt" family selected."""
+    return ns_path() == "nt" and mp % 256 == 0 and np_ % 256 == 0
+
+
 def default_sub_batch(n_tiles: int, mp: int, np_: int) -> int:
-    """Tiles per NS sub-batch: about 64 MiB of bf16 NS operand per launch, so
-    a sub-batch's X/A/B intermediates stay within MI355X's 256 MB MALL."""
+    """Tiles per NS sub-batch (one set of launches): about 256 MiB of bf16 NS
+    operand, so each launch has thousands of 256x256 blocks while a
+    sub-batch's A/B intermediates stay near the 256 MB MALL."""
     env = os.environ.get("HIMUON_NS_SUB_BATCH")
     if env:
         return max(1, min(n_tiles, int(env)))
-    target = 64 << 20
+    target = 256 << 20
     return max(1, min(n_tiles, target // (mp * np_ * 2)))
 
 
@@ -191,7 +209,7 @@ def make_desc_table(descs: list[ParamDesc], device) -> torch.Tensor:
 # ---------------------------------------------------------------------------
 # Entry points
 # ---------------------------------------------------------------------------
-def momentum_gather(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtype, tiles, partials):
+def momentum_gather(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtype, tiles, tiles_t, partials):
     _check(
         load().himuon_momentum_gather(
             desc_table.data_ptr(),
@@ -203,6 +221,7 @@ def momentum_gather(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtyp
             np_,
             dtype_code(dtype),
             tiles.data_ptr(),
+            _ptr(tiles_t),
             partials.data_ptr(),
             _stream(),
         ),
@@ -217,14 +236,18 @@ def tile_scale(partials, per_tile, n_tiles, inv, eps=NS_EPS):
     )
 
 
-def ns5(tiles_in, tiles_out, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, NS_B, NS_C)):
+def ns5(x, xt, y, yt, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, NS_B, NS_C)):
+    """NS5 on tiles x (and x^T in xt); X ping-pongs into y: the result is in x
+    for an even step count and in y for an odd one."""
     a, b, c = coeffs
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check(
         load().himuon_ns5(
-            tiles_in.data_ptr(),
-            tiles_out.data_ptr(),
+            x.data_ptr(),
+            _ptr(xt),
+            y.data_ptr(),
+            _ptr(yt),
             inv.data_ptr(),
             n_tiles,
             mp,

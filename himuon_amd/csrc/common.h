@@ -30,11 +30,24 @@ HM_DEV float f16_to_f32(uint16_t v) {
   return (float)h;
 }
 
+// fp32 -> fp16 bits, round to nearest even, in integer arithmetic (the
+// compiler cannot merge it with neighbouring fp32 operations).
 HM_DEV uint16_t f32_to_f16(float f) {
-  _Float16 h = (_Float16)f;
-  uint16_t v;
-  __builtin_memcpy(&v, &h, 2);
-  return v;
+  const uint32_t x = __float_as_uint(f);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);   // NaN
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // >= 65520 -> inf
+  if (ax >= 0x38800000u) {                                   // normal fp16
+    const uint32_t r = ax - 0x38000000u;                     // rebias 127 -> 15
+    return (uint16_t)(sign | ((r + 0x0fffu + ((r >> 13) & 1u)) >> 13));
+  }
+  const uint32_t e = ax >> 23;  // subnormal fp16 (or zero): units of 2^-24
+  if (e < 102) return (uint16_t)sign;
+  const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+  const uint32_t sh = 126 - e;  // 14..24
+  const uint32_t q = m >> sh, rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+  return (uint16_t)(sign | (q + ((rem > half) || (rem == half && (q & 1u)))));
 }
 
 // Load / store one element of a gradient-typed tensor as fp32.

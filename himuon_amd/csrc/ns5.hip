@@ -19,15 +19,11 @@
 // LDS with register prefetch of the next K slab. Blocks are mapped to XCDs so
 // all blocks of one NS tile share an L2.
 #include <algorithm>
+#include <cstdlib>
 
-#include "common.h"
+#include "ns5_kernels.h"
 
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int BM = 128, BN = 128, BK = 64;
@@ -37,20 +33,6 @@ HM_DEV f32x16_t mfma_32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
-
-// x -> bf16(x * s) for 8 packed bf16 values.
-HM_DEV u32x4_t scale8(u32x4_t v, float s) {
-  u32x4_t o;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float lo = bf16_to_f32(v[k] & 0xffffu) * s;
-    const float hi = __uint_as_float(v[k] & 0xffff0000u) * s;
-    o[k] = pack2(f32_to_bf16(lo), f32_to_bf16(hi));
-  }
-  return o;
-}
-
-HM_DEV uint32_t half16(uint32_t w, int h) { return h ? (w >> 16) : (w & 0xffffu); }
 
 // ---------------------------------------------------------------------------
 // C = bf16(alpha * S S^T + beta * S) for each tile; S is M x K (row pitch ldS),
@@ -304,17 +286,15 @@ __global__ __launch_bounds__(kThreads) void ns_scale_copy_kernel(const uint16_t*
 
 extern "C" size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np) {
   if (sub_batch <= 0 || mp <= 0 || np <= 0) return 0;
-  const size_t sq = (size_t)sub_batch * mp * mp * sizeof(uint16_t);
-  const size_t rect = (size_t)sub_batch * mp * np * sizeof(uint16_t);
-  return 2 * sq + 2 * rect;
+  return 2 * (size_t)sub_batch * mp * mp * sizeof(uint16_t);  // A and B per sub-batch tile
 }
 
-extern "C" int himuon_ns5(const uint16_t* tiles_in, uint16_t* tiles_out, const float* inv,
+extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, const float* inv,
                           int64_t n_tiles, int mp, int np, int steps, float a, float b, float c,
                           void* workspace, size_t workspace_bytes, int64_t sub_batch,
                           void* stream) {
-  if (!tiles_in || !tiles_out || !inv || n_tiles < 0 || steps < 0 || mp <= 0 || np <= 0 ||
-      mp > np || mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN || sub_batch <= 0)
+  if (!x || !y || x == y || !inv || n_tiles < 0 || steps < 0 || mp <= 0 || np <= 0 || mp > np ||
+      mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN || sub_batch <= 0 || (xt == nullptr) != (yt == nullptr))
     return HIMUON_EINVAL;
   if (n_tiles == 0) return 0;
   const int64_t sb = sub_batch < n_tiles ? sub_batch : n_tiles;
@@ -323,44 +303,58 @@ extern "C" int himuon_ns5(const uint16_t* tiles_in, uint16_t* tiles_out, const f
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t sq = (int64_t)mp * mp, rect = (int64_t)mp * np;
 
-  if (steps == 0) {
+  if (steps == 0) {  // X0 = bf16(x * inv), in place (the result of an even step count is in x)
     const int64_t nvec = n_tiles * rect / 8;
     const unsigned grid = (unsigned)std::min<int64_t>((nvec + kThreads - 1) / kThreads, 65536);
-    hipLaunchKernelGGL(ns_scale_copy_kernel, dim3(grid), dim3(kThreads), 0, s, tiles_in,
-                       tiles_out, inv, rect, n_tiles);
+    hipLaunchKernelGGL(ns_scale_copy_kernel, dim3(grid), dim3(kThreads), 0, s, x, x, inv, rect,
+                       n_tiles);
     return (int)hipGetLastError();
   }
 
   uint16_t* wsA = static_cast<uint16_t*>(workspace);
   uint16_t* wsB = wsA + sb * sq;
-  uint16_t* wsX[2] = {wsB + sb * sq, wsB + sb * sq + sb * rect};
+  // Kernel family: the per-block 256-block kernels when both edges allow
+  // 256-blocks, the persistent NT kernel when the caller also hands over X^T
+  // buffers, the 128-block kernels otherwise; HIMUON_NS_PATH=big|small
+  // overrides the choice (comparison runs).
+  const char* path = getenv("HIMUON_NS_PATH");
+  const bool force_big = path && path[0] == 'b', force_small = path && path[0] == 's';
+  const bool nt = xt && ns5_nt_supported(mp, np) && !force_big && !force_small;
+  const bool big = !nt && !force_small && ns5_nt_supported(mp, np);
   const int nb = mp / BM;
   const int npairs = nb * (nb + 1) / 2;
   const int apply_blocks = (mp / BM) * (np / BN);
 
   for (int64_t s0 = 0; s0 < n_tiles; s0 += sb) {
     const int64_t cnt = std::min<int64_t>(sb, n_tiles - s0);
-    const uint16_t* cur = tiles_in + s0 * rect;
-    uint16_t* out = tiles_out + s0 * rect;
-    const float* cur_inv = inv + s0;
-    const bool copy_back = (steps == 1 && cur == out);
-    for (int it = 0; it < steps; ++it) {
-      hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(cnt * npairs)), dim3(kThreads), 0,
-                         s, cur, rect, np, wsA, sq, mp, cur_inv, mp, np, cnt, 1.0f, 0.0f);
-      hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(cnt * npairs)), dim3(kThreads), 0,
-                         s, wsA, sq, mp, wsB, sq, mp, nullptr, mp, mp, cnt, c, b);
-      uint16_t* dst = (it == steps - 1 && !copy_back) ? out : wsX[it & 1];
-      hipLaunchKernelGGL(ns_apply_kernel, dim3((unsigned)xcd_grid(cnt * apply_blocks)),
-                         dim3(kThreads), 0, s, wsB, sq, cur, rect, dst, rect, cur_inv, mp, np, cnt,
-                         a);
-      cur = dst;
-      cur_inv = nullptr;
-    }
-    if (copy_back) {
-      const int64_t nvec = cnt * rect / 8;
-      const unsigned grid = (unsigned)std::min<int64_t>((nvec + kThreads - 1) / kThreads, 65536);
-      hipLaunchKernelGGL(ns_scale_copy_kernel, dim3(grid), dim3(kThreads), 0, s, cur, out,
-                         nullptr, rect, cnt);
+    const int64_t o = s0 * rect;
+    if (nt) {
+      ns5_nt_run(x + o, xt + o, y + o, yt + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
+    } else {
+      const uint16_t* cur = x + o;
+      uint16_t* nxt = y + o;
+      const float* cur_inv = inv + s0;
+      for (int it = 0; it < steps; ++it) {
+        if (big) {
+          ns5_launch_gram256(cur, rect, np, wsA, sq, mp, cur_inv, mp, np, cnt, 1.0f, 0.0f, s);
+          ns5_launch_gram256(wsA, sq, mp, wsB, sq, mp, nullptr, mp, mp, cnt, c, b, s);
+          ns5_launch_apply256(wsB, sq, cur, rect, nxt, rect, cur_inv, mp, np, cnt, a, s);
+        } else {
+          hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(cnt * npairs)),
+                             dim3(kThreads), 0, s, cur, rect, np, wsA, sq, mp, cur_inv, mp, np,
+                             cnt, 1.0f, 0.0f);
+          hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(cnt * npairs)),
+                             dim3(kThreads), 0, s, wsA, sq, mp, wsB, sq, mp, nullptr, mp, mp, cnt,
+                             c, b);
+          hipLaunchKernelGGL(ns_apply_kernel, dim3((unsigned)xcd_grid(cnt * apply_blocks)),
+                             dim3(kThreads), 0, s, wsB, sq, cur, rect, nxt, rect, cur_inv, mp, np,
+                             cnt, a);
+        }
+        const uint16_t* t = cur;
+        cur = nxt;
+        nxt = const_cast<uint16_t*>(t);
+        cur_inv = nullptr;
+      }
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;

@@ -84,90 +84,23 @@ HM_DEV float momentum_elem(float g, float* m, float mu, bool nesterov, bool has_
   const float mb = round_to<DT>(prod + g);
   *m = mb;
   if (!nesterov) return mb;
-  float e = __builtin_fmaf(mu, mb, g);
-  // Keep the fp32 rounding of the fma before the fp16 cast (the compiler
-  // would otherwise emit one fma with a direct fp16 result).
-  if constexpr (DT == HIMUON_DTYPE_F16) asm volatile("" : "+v"(e));
-  return round_to<DT>(e);
+  return round_to<DT>(__builtin_fmaf(mu, mb, g));
 }
 
 // ---------------------------------------------------------------------------
-// Gather, plain tiles (tile_h <= tile_w): NS (i, j) = tile (i, j).
-// Work item = (tile, slab of kSlabRows NS rows).
+// Gather: work item = (tile, 64x64 block of the NS operand). The block's
+// parameter elements are read as 16-byte row segments, momentum is applied,
+// and bf16(e) is written twice: in the parameter's orientation straight from
+// registers, and transposed through LDS. For plain tiles (tile_h <= tile_w)
+// the parameter orientation is X (the NS operand) and the transpose is X^T;
+// for tall tiles the NS operand is the tile's transpose, so the roles swap.
+// X^T (tiles_t, (n_tiles, np, mp)) is optional.
 // ---------------------------------------------------------------------------
-template <int DT>
-__global__ __launch_bounds__(kThreads) void gather_plain_kernel(
+template <int DT, bool TRANS>
+__global__ __launch_bounds__(kThreads) void gather_kernel(
     const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
-    uint16_t* __restrict__ tiles, float* __restrict__ partials) {
-  __shared__ float red[kThreads / 64];
-  const int slabs = geo.mp / kSlabRows;
-  const int64_t item = xcd_item(n_tiles * slabs);
-  if (item >= n_tiles * slabs) return;
-  const int64_t t = item / slabs;
-  const int q = (int)(item % slabs);
-  const HimuonParamDesc& P = params[find_param(params, n_params, t)];
-  const int64_t lt = t - P.tile0;
-  const int r = (int)(lt / P.C), c = (int)(lt % P.C);
-  const bool has_mom = P.momentum != nullptr;
-  const float mu = P.mu;
-  const bool nesterov = P.nesterov != 0;
-  const int vpr = geo.np / 8;  // 8-element vectors per NS row
-  uint16_t* out = tiles + t * (int64_t)geo.mp * geo.np;
-  float ssq = 0.f;
-  for (int v = threadIdx.x; v < kSlabRows * vpr; v += kThreads) {
-    const int i = q * kSlabRows + v / vpr;
-    const int j0 = (v % vpr) * 8;
-    const int64_t pr = (int64_t)r * geo.tile_h + i;
-    const int64_t pc = (int64_t)c * geo.tile_w + j0;
-    float x[8];
-    const bool row_ok = i < geo.tile_h && pr < P.h;
-    const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
-    const bool fast = row_ok && j0 + 8 <= geo.tile_w && pc + 8 <= P.w &&
-                      aligned16<DT>(P.grad, og) && (!has_mom || aligned16<DT>(P.momentum, om));
-    if (fast) {
-      float g[8], m[8];
-      load8<DT>(P.grad, og, g);
-      if (has_mom) load8<DT>(P.momentum, om, m);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = momentum_elem<DT>(g[e], &m[e], mu, nesterov, has_mom);
-      if (has_mom) store8<DT>(P.momentum, om, m);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x[e] = 0.f;
-        if (row_ok && j0 + e < geo.tile_w && pc + e < P.w) {
-          const float g = load_elem<DT>(P.grad, og + e);
-          float m = has_mom ? load_elem<DT>(P.momentum, om + e) : 0.f;
-          x[e] = momentum_elem<DT>(g, &m, mu, nesterov, has_mom);
-          if (has_mom) store_elem<DT>(P.momentum, om + e, m);
-        }
-      }
-    }
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t lo = f32_to_bf16(x[2 * k]), hi = f32_to_bf16(x[2 * k + 1]);
-      const float flo = bf16_to_f32(lo), fhi = bf16_to_f32(hi);
-      ssq = fmaf(flo, flo, ssq);
-      ssq = fmaf(fhi, fhi, ssq);
-      w[k] = pack2(lo, hi);
-    }
-    *reinterpret_cast<uint4*>(out + (int64_t)i * geo.np + j0) = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-  const float s = block_sum<kThreads>(ssq, red);
-  if (threadIdx.x == 0) partials[t * slabs + q] = s;
-}
-
-// ---------------------------------------------------------------------------
-// Gather, transposed tiles (tile_h > tile_w): NS (i, j) = tile (j, i).
-// Work item = (tile, 64x64 NS block); the block is transposed through LDS so
-// both the parameter reads and the NS writes are 16-byte row accesses.
-// ---------------------------------------------------------------------------
-template <int DT>
-__global__ __launch_bounds__(kThreads) void gather_trans_kernel(
-    const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
-    uint16_t* __restrict__ tiles, float* __restrict__ partials) {
-  __shared__ uint16_t sT[kBlk * kBlkPitch];  // [NS row i][NS col j]
+    uint16_t* __restrict__ tiles, uint16_t* __restrict__ tiles_t, float* __restrict__ partials) {
+  __shared__ uint16_t sT[kBlk * kBlkPitch];  // [param col][param row] of the block
   __shared__ float red[kThreads / 64];
   const int bi_n = geo.mp / kBlk, bj_n = geo.np / kBlk;
   const int blocks = bi_n * bj_n;
@@ -175,18 +108,24 @@ __global__ __launch_bounds__(kThreads) void gather_trans_kernel(
   if (item >= n_tiles * blocks) return;
   const int64_t t = item / blocks;
   const int b = (int)(item % blocks);
-  const int i0 = (b / bj_n) * kBlk, j0 = (b % bj_n) * kBlk;
+  const int i0 = (b / bj_n) * kBlk, j0 = (b % bj_n) * kBlk;  // NS block origin
+  const int tr0 = TRANS ? j0 : i0, tc0 = TRANS ? i0 : j0;     // tile-local origin
   const HimuonParamDesc& P = params[find_param(params, n_params, t)];
   const int64_t lt = t - P.tile0;
   const int r = (int)(lt / P.C), c = (int)(lt % P.C);
   const bool has_mom = P.momentum != nullptr;
   const float mu = P.mu;
   const bool nesterov = P.nesterov != 0;
+  const int64_t tsz = (int64_t)geo.mp * geo.np;
+  // Destination in the parameter orientation: X rows (plain) or X^T rows (tall).
+  uint16_t* direct = TRANS ? (tiles_t ? tiles_t + t * tsz : nullptr) : tiles + t * tsz;
+  const int direct_ld = TRANS ? geo.mp : geo.np;
+  uint16_t* across = TRANS ? tiles + t * tsz : (tiles_t ? tiles_t + t * tsz : nullptr);
+  const int across_ld = TRANS ? geo.np : geo.mp;
   float ssq = 0.f;
-  // Load: tile-local row tr = j0 + rr, cols tc = i0 + 8*cv .. +7.
   for (int v = threadIdx.x; v < kBlk * (kBlk / 8); v += kThreads) {
     const int rr = v / (kBlk / 8), cv = v % (kBlk / 8);
-    const int tr = j0 + rr, tc = i0 + cv * 8;
+    const int tr = tr0 + rr, tc = tc0 + cv * 8;
     const int64_t pr = (int64_t)r * geo.tile_h + tr;
     const int64_t pc = (int64_t)c * geo.tile_w + tc;
     const bool row_ok = tr < geo.tile_h && pr < P.h;
@@ -213,20 +152,25 @@ __global__ __launch_bounds__(kThreads) void gather_trans_kernel(
         }
       }
     }
+    uint32_t h[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const uint32_t h = f32_to_bf16(x[e]);
-      const float f = bf16_to_f32(h);
+      h[e] = f32_to_bf16(x[e]);
+      const float f = bf16_to_f32(h[e]);
       ssq = fmaf(f, f, ssq);
-      sT[(cv * 8 + e) * kBlkPitch + rr] = (uint16_t)h;
+      if (across) sT[(cv * 8 + e) * kBlkPitch + rr] = (uint16_t)h[e];
     }
+    if (direct)
+      *reinterpret_cast<uint4*>(direct + (int64_t)(tr0 + rr) * direct_ld + tc) =
+          make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
   }
-  __syncthreads();
-  uint16_t* out = tiles + t * (int64_t)geo.mp * geo.np;
-  for (int v = threadIdx.x; v < kBlk * (kBlk / 8); v += kThreads) {
-    const int ii = v / (kBlk / 8), jv = v % (kBlk / 8);
-    const uint4 q = *reinterpret_cast<const uint4*>(&sT[ii * kBlkPitch + jv * 8]);
-    *reinterpret_cast<uint4*>(out + (int64_t)(i0 + ii) * geo.np + j0 + jv * 8) = q;
+  if (across) {
+    __syncthreads();
+    for (int v = threadIdx.x; v < kBlk * (kBlk / 8); v += kThreads) {
+      const int cc = v / (kBlk / 8), rv = v % (kBlk / 8);
+      const uint4 q = *reinterpret_cast<const uint4*>(&sT[cc * kBlkPitch + rv * 8]);
+      *reinterpret_cast<uint4*>(across + (int64_t)(tc0 + cc) * across_ld + tr0 + rv * 8) = q;
+    }
   }
   const float s = block_sum<kThreads>(ssq, red);
   if (threadIdx.x == 0) partials[t * blocks + b] = s;
@@ -358,14 +302,13 @@ bool geo_ok(int tile_h, int tile_w, int mp, int np) {
 // ---------------------------------------------------------------------------
 extern "C" int himuon_gather_partials_per_tile(int tile_h, int tile_w, int mp, int np) {
   if (!geo_ok(tile_h, tile_w, mp, np)) return HIMUON_EINVAL;
-  if (tile_h > tile_w) return (mp / kBlk) * (np / kBlk);
-  return mp / kSlabRows;
+  return (mp / kBlk) * (np / kBlk);
 }
 
 extern "C" int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_params,
                                       int64_t n_tiles, int tile_h, int tile_w, int mp, int np,
-                                      int dtype, uint16_t* tiles_bf16, float* partials,
-                                      void* stream) {
+                                      int dtype, uint16_t* tiles_bf16, uint16_t* tiles_t_bf16,
+                                      float* partials, void* stream) {
   if (!geo_ok(tile_h, tile_w, mp, np) || n_params <= 0 || n_tiles < 0 || !params_dev ||
       !tiles_bf16 || !partials)
     return HIMUON_EINVAL;
@@ -375,13 +318,13 @@ extern "C" int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_p
   const bool trans = tile_h > tile_w;
   const int64_t items = n_tiles * himuon_gather_partials_per_tile(tile_h, tile_w, mp, np);
   const dim3 grid((unsigned)xcd_grid(items)), block(kThreads);
-#define HM_GATHER(DT)                                                                         \
-  if (trans)                                                                                  \
-    hipLaunchKernelGGL(gather_trans_kernel<DT>, grid, block, 0, s, params_dev, n_params,       \
-                       n_tiles, geo, tiles_bf16, partials);                     \
-  else                                                                                        \
-    hipLaunchKernelGGL(gather_plain_kernel<DT>, grid, block, 0, s, params_dev, n_params,       \
-                       n_tiles, geo, tiles_bf16, partials);
+#define HM_GATHER(DT)                                                                       \
+  if (trans)                                                                                \
+    hipLaunchKernelGGL((gather_kernel<DT, true>), grid, block, 0, s, params_dev, n_params,   \
+                       n_tiles, geo, tiles_bf16, tiles_t_bf16, partials);                   \
+  else                                                                                      \
+    hipLaunchKernelGGL((gather_kernel<DT, false>), grid, block, 0, s, params_dev, n_params,  \
+                       n_tiles, geo, tiles_bf16, tiles_t_bf16, partials);
   switch (dtype) {
     case HIMUON_DTYPE_F32: HM_GATHER(HIMUON_DTYPE_F32); break;
     case HIMUON_DTYPE_BF16: HM_GATHER(HIMUON_DTYPE_BF16); break;
@@ -412,7 +355,7 @@ extern "C" int himuon_untile(const HimuonParamDesc* params_dev, int n_params, in
   const Geo geo{tile_h, tile_w, mp, np};
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool trans = tile_h > tile_w;
-  const int64_t items = n_tiles * himuon_gather_partials_per_tile(tile_h, tile_w, mp, np);
+  const int64_t items = n_tiles * (trans ? (mp / kBlk) * (np / kBlk) : mp / kSlabRows);
   const dim3 grid((unsigned)xcd_grid(items)), block(kThreads);
 #define HM_UNTILE(DT)                                                                           \
   if (trans)                                                                                    \

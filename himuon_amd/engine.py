@@ -3,8 +3,9 @@
 A ``TileGroup`` owns everything one bucket of the HiMuon step needs on the
 device, allocated once so pointers stay stable for hipGraph capture:
 
-* the bf16 NS tile buffer ``(n_tiles, mp, np)`` (the concat buffer of
-  himuon.py:588-612, stored directly as the bf16 NS operand),
+* the bf16 NS tile buffers ``(n_tiles, mp, np)`` (the concat buffer of
+  himuon.py:588-612, stored directly as the bf16 NS operand) that X
+  ping-pongs between, plus their transposes when the NT kernel runs,
 * the per-tile sum-of-squares partials and normalisers,
 * the per-parameter ``update`` tensors (grad dtype) the untile kernel writes,
 * the device descriptor table (HimuonParamDesc[]) the gather/untile kernels read.
@@ -46,7 +47,14 @@ class TileGroup:
         self.tile0 = [sum(counts[:i]) for i in range(len(counts))]
         self.n_tiles = sum(counts)
         self.ppt = nat.gather_partials_per_tile(self.tile_h, self.tile_w, self.mp, self.np)
-        self.tiles = torch.empty((self.n_tiles, self.mp, self.np), device=device, dtype=torch.bfloat16)
+        shape, shape_t = (self.n_tiles, self.mp, self.np), (self.n_tiles, self.np, self.mp)
+        # X ping-pongs between tiles and alt through the NS iterations; the
+        # transposed copies exist only for the persistent NT kernel.
+        self.tiles = torch.empty(shape, device=device, dtype=torch.bfloat16)
+        self.alt = torch.empty(shape, device=device, dtype=torch.bfloat16)
+        nt = nat.nt_path(self.mp, self.np)
+        self.tiles_t = torch.empty(shape_t, device=device, dtype=torch.bfloat16) if nt else None
+        self.alt_t = torch.empty(shape_t, device=device, dtype=torch.bfloat16) if nt else None
         self.partials = torch.empty((self.n_tiles, self.ppt), device=device, dtype=torch.float32)
         self.inv = torch.empty((self.n_tiles,), device=device, dtype=torch.float32)
         self.updates = [torch.empty(g.shape, device=device, dtype=dtype) for g in grads]
@@ -104,20 +112,32 @@ class TileGroup:
     def gather(self) -> None:
         nat.momentum_gather(
             self.desc, len(self.updates), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
-            self.dtype, self.tiles, self.partials,
+            self.dtype, self.tiles, self.tiles_t, self.partials,
         )
         nat.tile_scale(self.partials, self.ppt, self.n_tiles, self.inv)
+
+    @staticmethod
+    def _rng(t, start, count):
+        return None if t is None else t[start : start + count]
 
     def ns(self, start: int, count: int, steps: int, workspace: torch.Tensor, sub_batch: int) -> None:
         if count <= 0:
             return
-        view = self.tiles[start : start + count]
-        nat.ns5(view, view, self.inv[start : start + count], count, self.mp, self.np, steps, workspace, sub_batch)
+        r = self._rng
+        nat.ns5(
+            r(self.tiles, start, count), r(self.tiles_t, start, count), r(self.alt, start, count),
+            r(self.alt_t, start, count), self.inv[start : start + count], count, self.mp, self.np, steps,
+            workspace, sub_batch,
+        )
 
-    def untile(self) -> None:
+    def result(self, steps: int) -> torch.Tensor:
+        """Buffer holding the NS output after `steps` iterations."""
+        return self.tiles if steps % 2 == 0 else self.alt
+
+    def untile(self, steps: int = 5) -> None:
         nat.untile(
             self.desc, len(self.updates), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
-            self.dtype, self.tiles,
+            self.dtype, self.result(steps),
         )
 
     def workspace_bytes(self, sub_batch: int) -> int:
@@ -156,5 +176,5 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     ws = torch.empty(max(1, grp.workspace_bytes(sb)), device=G.device, dtype=torch.uint8)
     grp.gather()
     grp.ns(0, grp.n_tiles, steps, ws, sb)
-    grp.untile()
+    grp.untile(steps)
     return out.view(G.shape).to(G.dtype)

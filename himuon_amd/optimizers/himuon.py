@@ -460,7 +460,7 @@ class HiMuon(Optimizer):
                 ns_launches += 1
                 total_B += c
                 ofs += c
-            grp.untile()
+            grp.untile(g["steps"])
             for (p, grp_dict), gi, upd in zip(g["entries"], g["group_idx"], grp.updates):
                 self._apply_wd_and_update(p, upd, grp_dict["weight_decay"], grp_dict["lr"], gi)
         ns_ms = 0.0

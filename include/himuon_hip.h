@@ -96,15 +96,18 @@ int himuon_gather_partials_per_tile(int tile_h, int tile_w, int mp, int np);
  * (fp32 arithmetic; rd = round to `dtype`; the buf update rounds its product
  * and sum separately, e is one fused multiply-add, as torch's in-place mul_,
  * add_ and add(alpha=) evaluate them). If momentum is NULL, e = g and
- * nothing is written back. bf16(e) is stored at its NS tile position; padding
- * is written as zero. partials[t * P + q] receives the fp32 sum of squares of
- * the bf16 values of the q-th slab of NS tile t, P =
+ * nothing is written back. bf16(e) is stored at its NS tile position in
+ * tiles_bf16 (n_tiles, mp, np) and, if tiles_t_bf16 is not NULL, at the
+ * transposed position in tiles_t_bf16 (n_tiles, np, mp); padding is written
+ * as zero. partials[t * P + q] receives the fp32 sum of squares of the bf16
+ * values of the q-th 64x64 block of NS tile t, P =
  * himuon_gather_partials_per_tile(...).
  */
 int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_params,
                            int64_t n_tiles, int tile_h, int tile_w, int mp,
                            int np, int dtype, uint16_t* tiles_bf16,
-                           float* partials, void* stream);
+                           uint16_t* tiles_t_bf16, float* partials,
+                           void* stream);
 
 /*
  * Per-tile normaliser: inv[t] = 1 / (sqrt(sum_q partials[t*P+q]) + eps).
@@ -114,30 +117,34 @@ int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_params,
 int himuon_tile_scale(const float* partials, int partials_per_tile,
                       int64_t n_tiles, float eps, float* inv, void* stream);
 
-/* Workspace bytes himuon_ns5 needs for a given sub-batch size. */
+/* Workspace bytes himuon_ns5 needs for a given sub-batch size (the A and B
+ * intermediates of `sub_batch` tiles). */
 size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np);
 
 /*
- * Batched quintic Newton-Schulz on n_tiles NS tiles (bf16, (n_tiles, mp, np)).
+ * Batched quintic Newton-Schulz on n_tiles NS tiles.
  * Replaces HiMuon.newton_schulz / _newton_schulz_3kernel / ns5_smem
  * (himuon.py:232-284; triton_kernels/XXT.py:13-75, ba_plus_cAA.py:13-89,
  * fused_bmm_add.py:13-96, ns5_smem.py:46-104).
  *
- *   X0 = bf16(x * inv[t])                 (x = tiles_in, i.e. bf16 of the tile)
+ *   X0 = bf16(x * inv[t])                 (x = the gathered bf16 tile)
  *   repeat `steps` times:
  *     A = bf16(X X^T)                       fp32 accumulation
  *     B = bf16(c * (A A^T) + b * A)          fp32 accumulation / epilogue
  *     X = bf16(bf16(B X) + a * X)
- *   tiles_out = X
  *
- * tiles_out may equal tiles_in. Tiles are processed in sub-batches of
- * `sub_batch`; the workspace must hold himuon_ns5_workspace_bytes(sub_batch,
- * mp, np) bytes. steps == 0 writes X0.
+ * x, y: (n_tiles, mp, np) bf16; X ping-pongs between them, so the result is
+ * in x when `steps` is even and in y when it is odd (x is overwritten).
+ * xt, yt: optional (n_tiles, np, mp) transposed copies (both or neither);
+ * xt must hold X0^T as written by himuon_momentum_gather. With them, tiles
+ * whose mp and np are multiples of 256 run on the persistent 256-block path.
+ * Tiles are processed in sub-batches of `sub_batch`; the workspace must hold
+ * himuon_ns5_workspace_bytes(sub_batch, mp, np) bytes.
  */
-int himuon_ns5(const uint16_t* tiles_in, uint16_t* tiles_out, const float* inv,
-               int64_t n_tiles, int mp, int np, int steps, float a, float b,
-               float c, void* workspace, size_t workspace_bytes,
-               int64_t sub_batch, void* stream);
+int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt,
+               const float* inv, int64_t n_tiles, int mp, int np, int steps,
+               float a, float b, float c, void* workspace,
+               size_t workspace_bytes, int64_t sub_batch, void* stream);
 
 /*
  * Untile/scatter: for every element of every parameter,

@@ -61,7 +61,18 @@ GATHER_CASES = [
     ("fp16", [(384, 640)], 128, 128, "float16", True),
     ("full_tall_fp32", [(2048, 1024)], 2048, 1024, "float32", True),
     ("odd_small", [(7, 50), (50, 7)], 16, 16, "float32", True),
+    ("nt_512_mixed", [(1024, 1536), (700, 300)], 512, 512, "float32", True),
+    ("nt_tall_tiles", [(1024, 512)], 512, 256, "bfloat16", True),
 ]
+
+
+@pytest.fixture(params=["big", "nt", "small"])
+def ns_family(request, monkeypatch):
+    """Run a test under each NS kernel family (256-blocks, persistent NT with
+    X^T buffers, 128-blocks); shapes a family cannot take fall back to the
+    128-block kernels."""
+    monkeypatch.setenv("HIMUON_NS_PATH", request.param)
+    return request.param
 
 
 def _make_group(shapes, th, tw, dtype, nesterov, seed, mus=None, with_mom=True):
@@ -78,8 +89,9 @@ def _make_group(shapes, th, tw, dtype, nesterov, seed, mus=None, with_mom=True):
 
 
 @pytest.mark.parametrize("name,shapes,th,tw,dtype,nesterov", GATHER_CASES, ids=[c[0] for c in GATHER_CASES])
-def test_gather_bit_exact(name, shapes, th, tw, dtype, nesterov):
+def test_gather_bit_exact(name, shapes, th, tw, dtype, nesterov, monkeypatch):
     print(f"[gather] {name}", flush=True)
+    monkeypatch.setenv("HIMUON_NS_PATH", "nt")  # also check X^T where the tiles allow it
     mus = [0.95, 0.9, 0.8][: len(shapes)]
     grp, grads, moms = _make_group(shapes, th, tw, dtype, nesterov, seed=10, mus=mus)
     g_np = [g.float().cpu().numpy() for g in grads]
@@ -94,6 +106,9 @@ def test_gather_bit_exact(name, shapes, th, tw, dtype, nesterov):
         exp = _ns_layout(O.tile(O.bf16_round(ge), th, tw), grp.mp, grp.np)
         got = tiles[ofs : ofs + exp.shape[0]]
         assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), f"tiles param {i}"
+        if grp.tiles_t is not None:
+            got_t = grp.tiles_t[ofs : ofs + exp.shape[0]].float().cpu().numpy()
+            assert np.array_equal(got_t, np.swapaxes(exp, 1, 2)), f"transposed tiles param {i}"
         ofs += exp.shape[0]
     assert ofs == grp.n_tiles
     # per-tile norm and normaliser
@@ -119,7 +134,7 @@ def test_untile_bit_exact(name, shapes, th, tw, dtype, nesterov):
     grp.tiles.copy_(vals.to(DEV))
     for u in grp.updates:
         u.fill_(float("nan"))
-    grp.untile()
+    grp.untile(steps=0)  # even step count: the result buffer is grp.tiles
     torch.cuda.synchronize()
     v = vals.float().numpy()
     ofs = 0
@@ -156,11 +171,11 @@ NS_SHAPES = [
 
 
 @pytest.mark.parametrize("label,shape", NS_SHAPES, ids=[s[0] for s in NS_SHAPES])
-def test_newton_schulz_matches_reference_on_well_conditioned(label, shape):
+def test_newton_schulz_matches_reference_on_well_conditioned(label, shape, ns_family):
     """HiMuon.newton_schulz == the reference's NS in bf16 on well-conditioned
     inputs, with the reference test's elementwise tolerance (4e-2) and the
     north star's per-tile relative Frobenius bound (1e-2)."""
-    print(f"[ns5 wc] {label} {shape}", flush=True)
+    print(f"[ns5 wc] {label} {shape} {ns_family}", flush=True)
     G = well_conditioned(shape, torch.bfloat16, seed=0)
     out = _ns_engine(G)
     assert out.shape == G.shape and out.dtype == G.dtype
@@ -174,11 +189,11 @@ def test_newton_schulz_matches_reference_on_well_conditioned(label, shape):
 
 
 @pytest.mark.parametrize("T,n", [(128, 32), (256, 16), (512, 8)])
-def test_ns5_random_tiles_vs_oracle_and_torch(T, n):
+def test_ns5_random_tiles_vs_oracle_and_torch(T, n, ns_family):
     """Random (momentum-like) tiles: per-tile error against the torch
     same-dtype NS5 and the CPU oracle, next to the distance between those two
     references themselves (the summation-order noise floor of bf16 NS5)."""
-    print(f"[ns5 random] T={T} n={n}", flush=True)
+    print(f"[ns5 random] T={T} n={n} {ns_family}", flush=True)
     G = _cpu_randn((n, T, T), seed=T, scale=1e-3).to(DEV)
     out = _ns_engine(G)
     ref_t = ns5_torch_staged(G)
@@ -195,7 +210,7 @@ def test_ns5_random_tiles_vs_oracle_and_torch(T, n):
 
 
 @pytest.mark.parametrize("T,n", [(128, 16), (512, 4)])
-def test_ns5_singular_value_band(T, n):
+def test_ns5_singular_value_band(T, n, ns_family):
     G = _cpu_randn((n, T, T), seed=T + 1, scale=1e-3).to(DEV)
     out = _ns_engine(G).double()
     sv = torch.linalg.svdvals(out).cpu().numpy()
@@ -213,7 +228,7 @@ def test_ns5_singular_value_band(T, n):
         assert abs(np.sort(sv[k])[nn_] - np.sort(ref_sv[k])[nn_]) < 0.05
 
 
-def test_ns5_zero_tile_and_padding():
+def test_ns5_zero_tile_and_padding(ns_family):
     # zero tiles map to zero (0 / (0 + eps) = 0); zero padding stays zero and
     # does not change the data block (a 37x100 block in a 256x256 tile equals
     # the same block NS'd in its own 128x128 padding, bit for bit)
@@ -227,26 +242,24 @@ def test_ns5_zero_tile_and_padding():
 
 
 @pytest.mark.parametrize("steps", [0, 1, 2, 5])
-def test_ns5_steps_honoured(steps):
-    G = _cpu_randn((2, 128, 256), seed=9).to(DEV)
+def test_ns5_steps_honoured(steps, ns_family):
+    G = _cpu_randn((2, 256, 512), seed=9).to(DEV)
     out = _ns_engine(G, steps=steps)
     ref = torch.from_numpy(O.ns5_staged(G.cpu().numpy(), steps=steps)).to(DEV)
     assert per_tile_rel_fro(out, ref).max() <= 1.5e-2
 
 
-def test_ns5_sub_batch_invariance():
+def test_ns5_sub_batch_invariance(ns_family):
     """Sub-batching (tiles are independent) does not change results bitwise."""
     G = _cpu_randn((10, 256, 256), seed=12, scale=1e-3).to(DEV)
     grp = TileGroup([G.view(-1, 256)], [G.view(-1, 256)], [None], 256, 256, [1.0], [0.0], [False],
                     torch.device(DEV), torch.float32)
-    grp.gather()
-    base = grp.tiles.clone()
     outs = []
     for sb in (1, 3, 10):
-        grp.tiles.copy_(base)
+        grp.gather()  # NS overwrites both X orientations (ping-pong): re-gather each run
         ws = torch.empty(grp.workspace_bytes(sb), device=DEV, dtype=torch.uint8)
         grp.ns(0, grp.n_tiles, 5, ws, sb)
-        outs.append(grp.tiles.clone())
+        outs.append(grp.result(5).clone())
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
 
 
