@@ -319,8 +319,10 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
   // overrides the choice (comparison runs).
   const char* path = getenv("HIMUON_NS_PATH");
   const bool force_big = path && path[0] == 'b', force_small = path && path[0] == 's';
-  const bool nt = xt && ns5_nt_supported(mp, np) && !force_big && !force_small;
-  const bool big = !nt && !force_small && ns5_nt_supported(mp, np);
+  const bool force_pk = path && path[0] == 'p';
+  const bool pk = force_pk && ns5_pk_supported(mp, np);
+  const bool nt = !pk && xt && ns5_nt_supported(mp, np) && !force_big && !force_small;
+  const bool big = !pk && !nt && !force_small && ns5_nt_supported(mp, np);
   const int nb = mp / BM;
   const int npairs = nb * (nb + 1) / 2;
   const int apply_blocks = (mp / BM) * (np / BN);
@@ -328,7 +330,9 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
   for (int64_t s0 = 0; s0 < n_tiles; s0 += sb) {
     const int64_t cnt = std::min<int64_t>(sb, n_tiles - s0);
     const int64_t o = s0 * rect;
-    if (nt) {
+    if (pk) {
+      ns5_pk_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
+    } else if (nt) {
       ns5_nt_run(x + o, xt + o, y + o, yt + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
     } else {
       const uint16_t* cur = x + o;

@@ -66,7 +66,7 @@ GATHER_CASES = [
 ]
 
 
-@pytest.fixture(params=["big", "nt", "small"])
+@pytest.fixture(params=["big", "nt", "pk", "small"])
 def ns_family(request, monkeypatch):
     """Run a test under each NS kernel family (256-blocks, persistent NT with
     X^T buffers, 128-blocks); shapes a family cannot take fall back to the
