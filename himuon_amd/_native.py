@@ -172,10 +172,10 @@ def ns5_workspace_bytes(sub_batch: int, mp: int, np_: int) -> int:
 
 
 def ns_path() -> str:
-    """NS kernel family: HIMUON_NS_PATH = "big" (256-blocks, the default for
-    256-aligned tiles), "nt" (persistent 256-block kernel reading X and X^T)
-    or "small" (128-blocks for every shape)."""
-    return os.environ.get("HIMUON_NS_PATH", "big")
+    """NS kernel family for 256-aligned tiles: HIMUON_NS_PATH = "stream"
+    (persistent streamed-operand kernels, the default), "big", "pk", "nt"
+    (persistent kernel reading X and X^T) or "small" (128-blocks)."""
+    return os.environ.get("HIMUON_NS_PATH", "stream")
 
 
 def nt_path(mp: int, np_: int) -> bool:
@@ -186,13 +186,13 @@ def nt_path(mp: int, np_: int) -> bool:
 
 
 def default_sub_batch(n_tiles: int, mp: int, np_: int) -> int:
-    """Tiles per NS sub-batch (one set of launches): about 256 MiB of bf16 NS
-    operand, so each launch has thousands of 256x256 blocks while a
-    sub-batch's A/B intermediates stay near the 256 MB MALL."""
+    """Tiles per NS sub-batch (one set of launches): about 2 GiB of bf16 NS
+    operand (4096 tiles of 512x512), so each launch has >10k 256x256 blocks
+    and launch tails stay small; the A/B workspace is twice that."""
     env = os.environ.get("HIMUON_NS_SUB_BATCH")
     if env:
         return max(1, min(n_tiles, int(env)))
-    target = 256 << 20
+    target = 2 << 30
     return max(1, min(n_tiles, target // (mp * np_ * 2)))
 
 

@@ -313,16 +313,17 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
 
   uint16_t* wsA = static_cast<uint16_t*>(workspace);
   uint16_t* wsB = wsA + sb * sq;
-  // Kernel family: the per-block 256-block kernels when both edges allow
-  // 256-blocks, the persistent NT kernel when the caller also hands over X^T
-  // buffers, the 128-block kernels otherwise; HIMUON_NS_PATH=big|small
-  // overrides the choice (comparison runs).
+  // Kernel family for tiles whose padded edges are multiples of 256: the
+  // persistent streamed-operand kernels by default; HIMUON_NS_PATH =
+  // big | nt | pk | small selects another family (comparison runs; nt also
+  // needs the caller's X^T buffers). Other tiles run the 128-block kernels.
   const char* path = getenv("HIMUON_NS_PATH");
-  const bool force_big = path && path[0] == 'b', force_small = path && path[0] == 's';
-  const bool force_pk = path && path[0] == 'p';
-  const bool pk = force_pk && ns5_pk_supported(mp, np);
-  const bool nt = !pk && xt && ns5_nt_supported(mp, np) && !force_big && !force_small;
-  const bool big = !pk && !nt && !force_small && ns5_nt_supported(mp, np);
+  const char p0 = path ? path[0] : 0;
+  const bool al256 = ns5_stream_supported(mp, np);
+  const bool st = al256 && (p0 == 0 || p0 == 's' && path[1] == 't');
+  const bool pk = al256 && p0 == 'p';
+  const bool nt = al256 && p0 == 'n' && xt;
+  const bool big = al256 && (p0 == 'b' || (p0 == 'n' && !xt));
   const int nb = mp / BM;
   const int npairs = nb * (nb + 1) / 2;
   const int apply_blocks = (mp / BM) * (np / BN);
@@ -330,7 +331,9 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
   for (int64_t s0 = 0; s0 < n_tiles; s0 += sb) {
     const int64_t cnt = std::min<int64_t>(sb, n_tiles - s0);
     const int64_t o = s0 * rect;
-    if (pk) {
+    if (st) {
+      ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
+    } else if (pk) {
       ns5_pk_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
     } else if (nt) {
       ns5_nt_run(x + o, xt + o, y + o, yt + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);

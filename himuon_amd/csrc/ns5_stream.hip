@@ -1,0 +1,524 @@
+// Persistent streamed-operand kernels for the three NS5 stages on 256x256
+// output blocks (NS tiles whose padded edges are multiples of 256):
+//
+//   GramA : C = A = bf16(X X^T)            P = Q = X (rows, K = n)   lower blocks + mirror
+//   GramB : C = B = bf16(c A A^T + b A)    P = Q = A (rows, K = m)   lower blocks + mirror
+//   Apply : C = X' = bf16(bf16(B X) + a X) P = B (rows, K = m), Q = X read as [k][j]
+// (ns5_smem.py:89-101, XXT.py:55-75, ba_plus_cAA.py:58-85, fused_bmm_add.py:65-88).
+//
+// One 256-thread workgroup per CU (4 waves in 2x2, each a 128x128 sub-block
+// of 4x4 v_mfma_f32_32x32x16_bf16 tiles, 256 fp32 accumulators per lane)
+// walks a contiguous range of output blocks of its XCD.
+//
+// Operand stream. K advances in units of 32. Each unit of P (and Q) goes
+// straight from global memory into a 32 KiB slot of a 5-slot LDS ring
+// (global_load_lds_dwordx4, 1 KiB per wave instruction); loads run 4 units
+// ahead of the MFMAs, so up to 128 KiB per CU are in flight. The epilogue
+// operand R (A for GramB, X for Apply) is streamed behind the last K unit as
+// four more 32 KiB units (64 rows x 256 columns each), so it lands while the
+// last MFMAs run. A direct load writes lane l's 16 bytes at 16 l of the wave's
+// 1 KiB, so LDS bank spreading is done by choosing which 16-byte source chunk
+// each lane fetches (a per-row XOR swizzle of the chunk index).
+//
+// MFMA operands are swapped (A operand = rows j, B operand = rows i), so lane
+// l holds C[row l%32][4 consecutive columns]. The epilogue converts in
+// registers, stages each wave's 128x128 bf16 result in its own 32 KiB of LDS
+// and writes it with 16-byte row-contiguous stores (256 bytes per row). Off-
+// diagonal Gram blocks also write the mirrored block: a 4x4 transpose across
+// each lane quad (two DPP exchanges) restages the sub-block as rows of C^T.
+#include "ns5_kernels.h"
+
+namespace {
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __attribute__((address_space(3))) const u32x4_t lds_cu32x4;
+typedef __attribute__((address_space(3))) const u32x2_t lds_cu32x2;
+typedef __attribute__((address_space(3))) u32x2_t lds_u32x2;
+
+constexpr int NT = 256;
+constexpr int BT = 256;               // output block edge
+constexpr int BK = 32;                // K per stream unit
+constexpr int SLOT = 32768;           // bytes per ring slot
+constexpr int NSLOT = 5;              // ring slots
+constexpr int DIST = NSLOT - 1;       // units in flight ahead of the MFMAs
+constexpr int LDS_BYTES = NSLOT * SLOT;
+constexpr int HALF = SLOT / 2;        // Q panel offset within a slot
+
+enum { kGramA = 0, kGramB = 1, kApply = 2 };
+
+struct StArgs {
+  const uint16_t* P; int64_t p_bs; int ldp;    // rows i (output rows), k-contiguous
+  const uint16_t* Q; int64_t q_bs; int ldq;    // Gram: rows j, k-contiguous; Apply: X [k][j]
+  const uint16_t* R; int64_t r_bs; int ldr;    // epilogue operand [i][j] (A or X)
+  uint16_t* C; int64_t c_bs; int ldc;          // output [i][j]
+  int M, N, K;
+  int64_t ntiles;
+  float alpha, beta;                           // GramB: c, b; Apply: beta = a
+};
+
+HM_DEV f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// bf16 pair (RNE, hardware v_cvt_pk_bf16_f32): lo in bits 0..15.
+HM_DEV uint32_t pk_bf16(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t r;
+  r[0] = (__bf16)lo;
+  r[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// s_waitcnt with vmcnt = N (expcnt and lgkmcnt at their maxima) / lgkmcnt = N.
+template <int N>
+HM_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+template <int N>
+HM_DEV void wait_lgkm() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));
+}
+
+// Workgroup barrier for LDS reuse: this wave's LDS operations are complete;
+// global memory operations (including direct-to-LDS loads) may still be in
+// flight and are waited for explicitly with vmcnt. (__syncthreads() lowers
+// to a fence that waits for every outstanding load and store, which would
+// drain the operand stream at each barrier.)
+HM_DEV void lds_barrier() {
+  wait_lgkm<0>();
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// Direct-to-LDS 16-byte load: lane l's 16 bytes from gptr land at LDS byte
+// lds_wave + 16 l (lds_wave is wave-uniform, passed in M0). Issued as inline
+// assembly: the compiler models the builtin as a flat access to both global
+// memory and LDS and, while one is pending, forces lgkmcnt(0)/vmcnt(0) waits
+// before unrelated LDS reads. Completion is tracked by vmcnt (in issue order
+// with the other vector loads) and waited for explicitly.
+HM_DEV void dma16(const void* gptr, uint32_t lds_wave) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(gptr), "s"(__builtin_amdgcn_readfirstlane(lds_wave))
+      : "memory", "m0");
+}
+
+// ds_read_b64_tr_b16 at an LDS byte address. Issued as inline assembly: the
+// compiler cannot tell these reads apart from the direct-to-LDS loads in
+// flight and would put a vmcnt(0) wait (draining the operand stream) before
+// the builtin. The result is only valid after an explicit lgkmcnt wait.
+HM_DEV u32x2_t ds_read_tr16(uint32_t addr) {
+  u32x2_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+// DPP quad permutations.
+HM_DEV uint32_t quad_swap2(uint32_t v) {  // lane ^ 2
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+}
+HM_DEV uint32_t quad_swap1(uint32_t v) {  // lane ^ 1
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+}
+
+// 4x4 bf16 transpose across a lane quad: lane k holds row k as (w0, w1) =
+// columns (0,1), (2,3); returns column k as rows (0,1), (2,3).
+HM_DEV u32x2_t quad_transpose(u32x2_t w, int k) {
+  const uint32_t send_a = (k < 2) ? w[1] : w[0];
+  const uint32_t recv_a = quad_swap2(send_a);
+  const uint32_t x = (k < 2) ? w[0] : recv_a;
+  const uint32_t y = (k < 2) ? recv_a : w[1];
+  const bool odd = k & 1;
+  const uint32_t send_b = odd ? ((x & 0xffffu) | (y << 16)) : ((x >> 16) | (y & 0xffff0000u));
+  const uint32_t r = quad_swap1(send_b);
+  u32x2_t o;
+  if (odd) {
+    o[0] = (r & 0xffffu) | (x & 0xffff0000u);
+    o[1] = (r >> 16) | (y & 0xffff0000u);
+  } else {
+    o[0] = (x & 0xffffu) | (r << 16);
+    o[1] = (y & 0xffffu) | (r & 0xffff0000u);
+  }
+  return o;
+}
+
+// Chunk swizzles (16-byte chunk index XOR a function of the row):
+//  P/Q row panels, 64-byte rows: spreads 8 (or 16) consecutive rows of one
+//  chunk over distinct bank groups for 32- and 64-bank layouts;
+//  X panel of Apply, 512-byte rows: the transposing reads of 4 rows x 32
+//  bytes hit distinct bank groups;
+//  R units and the output staging, 512/256-byte rows: consecutive rows of
+//  one chunk land in distinct bank groups.
+HM_DEV int swz_p(int r) { return (((r >> 1) ^ (r >> 3)) & 1) | (((r >> 2) & 1) << 1); }
+HM_DEV int swz_x(int r) { return 10 * (r & 1) + 4 * ((r >> 1) & 1); }
+HM_DEV int swz_c(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// vmcnt while waiting for unit w: loads of the (up to DIST - 1) units issued
+// after it. A K unit is L loads per wave, an R unit 8.
+template <int L, int NR>
+HM_DEV void wait_unit(int nk, int w) {
+  const int rem = nk - 1 - w;
+  if (rem >= 3) {
+    wait_vm<3 * L>();
+  } else if (rem == 2) {
+    wait_vm<2 * L + (NR >= 1 ? 8 : 0)>();
+  } else if (rem == 1) {
+    wait_vm<L + (NR >= 2 ? 16 : 8 * NR)>();
+  } else {
+    wait_vm<(NR >= 3 ? 24 : 8 * NR)>();
+  }
+}
+
+// One 256x256 output block C[tile][bi-block][bj-block]. DIAG: Gram diagonal
+// block, Q = P (one panel streamed), no mirror.
+template <int MODE, bool DIAG, int NKC>
+__device__ __forceinline__ void st_item(const StArgs& g, lds_u8* lds, int64_t tile, int bi, int bj) {
+  constexpr bool kTr = MODE == kApply;
+  constexpr int NR = (MODE == kGramA) ? 0 : 4;  // R units
+  constexpr int L = DIAG ? 4 : 8;               // K-unit loads per wave
+  // The lane index is made opaque per block so that the per-lane addresses
+  // below are recomputed for each block instead of being hoisted out of the
+  // persistent loop (where they would not fit in registers).
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int nk = NKC > 0 ? NKC : g.K / BK;  // K units (compile-time for the common K)
+  const int U = nk + NR;
+
+  // ---- loaders ------------------------------------------------------------
+  // Row panel (256 rows x 64 B): wave instruction n = 4 i + wave fills rows
+  // 16 n .. 16 n + 15; lane l lands at row 16 n + l/4, position l%4 and
+  // fetches chunk (l%4) ^ swz_p(row) (row & 15 = l/4).
+  const int prl = lane >> 2;
+  const int pch = (lane & 3) ^ swz_p(prl);
+  const uint16_t* psrc = g.P + tile * g.p_bs + (int64_t)(bi * BT + 16 * wave + prl) * g.ldp + pch * 8;
+  const int64_t pstep = 64 * (int64_t)g.ldp;
+  const uint16_t* qsrc;
+  int64_t qstep, qunit;
+  if constexpr (kTr) {
+    // X panel (32 k-rows x 512 B): instruction n fills k-rows 2n, 2n + 1;
+    // lane l lands at row 2n + l/32, position l%32, fetching chunk
+    // (l%32) ^ swz_x(row) (row & 3 = (2 wave + hi) & 3).
+    const int xr = 2 * wave + hi;
+    const int xc = l32 ^ swz_x(xr);
+    qsrc = g.Q + tile * g.q_bs + (int64_t)xr * g.ldq + bj * BT + xc * 8;
+    qstep = 8 * (int64_t)g.ldq;
+    qunit = BK * (int64_t)g.ldq;
+  } else {
+    qsrc = g.Q + tile * g.q_bs + (int64_t)(bj * BT + 16 * wave + prl) * g.ldq + pch * 8;
+    qstep = 64 * (int64_t)g.ldq;
+    qunit = BK;
+  }
+  // R unit q (block rows 64 q .. 64 q + 63, 256 columns, 512-byte rows):
+  // instruction n = 4 i + wave fills rows 2n, 2n + 1; chunk (l%32) ^ (row & 15).
+  const uint16_t* rsrc = nullptr;
+  if constexpr (NR > 0)
+    rsrc = g.R + tile * g.r_bs + (int64_t)(bi * BT + 2 * wave + hi) * g.ldr + bj * BT;
+  const uint32_t wdst = (uint32_t)(uintptr_t)lds + wave * 1024;
+
+  auto issue = [&](int v) {
+    const uint32_t d = wdst + (v % NSLOT) * SLOT;
+    if (v < nk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dma16(psrc + i * pstep + v * BK, d + i * 4096);
+      if constexpr (!DIAG) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          dma16(qsrc + i * qstep + v * qunit, d + HALF + i * 4096);
+      }
+    } else if constexpr (NR > 0) {
+      const int q = v - nk;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int sw = 8 * (i & 1) + 2 * wave + hi;  // (64 q + 8 i + 2 wave + hi) & 15
+        const uint16_t* s = rsrc + (int64_t)(64 * q + 8 * i) * g.ldr + ((l32 ^ sw) * 8);
+        dma16(s, d + i * 4096);
+      }
+    }
+  };
+
+  // ---- MFMA fragments of unit v, sub-step ks --------------------------------
+  // B operand (rows i = wm*128 + 32 t + l32 of P): k-chunk 2 ks + hi. A
+  // operand: the same from Q (rows j) for Gram; for Apply two transposing
+  // reads of the X panel (ds_read_b64_tr_b16: within 16 lanes, lane 4a+b
+  // receives element b of the 8-byte rows addressed by lanes a, a+4, a+8,
+  // a+12), giving lane l column j = wn*128 + 32 t + l%32, k = 16 ks + 8 hi + 0..7.
+  const int sp = swz_p(l32 & 15);
+  const int prow = (wm * 128 + l32) * 64, qrow = (wn * 128 + l32) * 64;
+  const int r16 = lane & 15, te = r16 >> 2;
+  const int tr_s = swz_x(te);
+  const int tr_row = 8 * hi + te;
+  const int tr_chunk = wn * 16 + 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
+  const int tr_sub = (r16 & 1) * 8;
+  auto frags = [&](int v, int ks, u32x4_t(&fa)[4], u32x4_t(&fb)[4]) {
+    const lds_u8* s = lds + (v % NSLOT) * SLOT;
+    const int pos = ((2 * ks + hi) ^ sp) * 16;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) fb[t] = *reinterpret_cast<lds_cu32x4*>(s + prow + t * 2048 + pos);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if constexpr (kTr) {
+        const uint32_t off = (uint32_t)(uintptr_t)s + HALF + (16 * ks + tr_row) * 512 +
+                             (((tr_chunk + 4 * t) ^ tr_s) * 16) + tr_sub;
+        const u32x2_t l2 = ds_read_tr16(off), u2 = ds_read_tr16(off + 4 * 512);
+        fa[t] = u32x4_t{l2[0], l2[1], u2[0], u2[1]};
+      } else {
+        const lds_u8* qs = DIAG ? s : s + HALF;
+        fa[t] = *reinterpret_cast<lds_cu32x4*>(qs + qrow + t * 2048 + pos);
+      }
+    }
+  };
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+  auto mma = [&](const u32x4_t(&fa)[4], const u32x4_t(&fb)[4]) {
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) acc[tj][ti] = mfma(fa[tj], fb[ti], acc[tj][ti]);
+  };
+
+  // ---- K loop ------------------------------------------------------------------
+  // Unit u lives in slot u % NSLOT. At the top of unit u + 1 each wave waits
+  // for its own loads of that unit, then the barrier publishes the unit and
+  // frees slot u % NSLOT (every wave has its unit-u fragments in registers),
+  // which receives unit u + 1 + DIST. The second half of unit u's MFMAs runs
+  // after the barrier, covering the first fragment reads of unit u + 1.
+  lds_barrier();  // the previous block's epilogue is done with the LDS
+#pragma unroll
+  for (int v = 0; v < DIST; ++v) issue(v);
+  wait_unit<L, NR>(nk, 0);
+  lds_barrier();
+  issue(DIST);
+  u32x4_t fa0[4], fb0[4], fa1[4], fb1[4];
+  // At most one half-unit of fragment reads is in flight at any time (8 or 12
+  // LDS operations: lgkmcnt counts to 15). Unit u: the first-half fragments
+  // have landed at its start and the second-half reads are in flight; each
+  // half's reads are issued ahead of the other half's 16 MFMAs.
+  frags(0, 0, fa0, fb0);
+  wait_lgkm<0>();
+  __builtin_amdgcn_sched_barrier(0);
+  frags(0, 1, fa1, fb1);
+  __builtin_amdgcn_sched_barrier(0);
+  auto unit = [&](int u) {
+    mma(fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lgkm<0>();  // second-half fragments of unit u
+    wait_unit<L, NR>(nk, u + 1);
+    lds_barrier();
+    if (u + 1 + DIST < U) issue(u + 1 + DIST);
+    frags(u + 1, 0, fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lgkm<0>();  // first-half fragments of unit u + 1
+    frags(u + 1, 1, fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if constexpr (NKC > 0) {
+#pragma unroll
+    for (int u = 0; u + 1 < NKC; ++u) unit(u);
+  } else {
+    for (int u = 0; u + 1 < nk; ++u) unit(u);
+  }
+  mma(fa0, fb0);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_lgkm<0>();
+  mma(fa1, fb1);
+
+  // ---- epilogue ------------------------------------------------------------------
+  // out[ti][tj][q] = 4 bf16 of C[i][j..j+3], i = wm*128 + 32 ti + l32,
+  // j = wn*128 + 32 tj + 8 q + 4 hi (block-local).
+  u32x2_t out[4][4][4];
+  if constexpr (NR > 0) {
+    wait_vm<0>();
+    lds_barrier();  // every wave's R loads have landed
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      const int il = wm * 128 + 32 * ti + l32;
+      const int rq = il & 63;
+      const lds_u8* rs = lds + ((nk + (il >> 6)) % NSLOT) * SLOT + rq * 512 + hi * 8;
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int ch = wn * 16 + 4 * tj + q;
+          const u32x2_t rv = *reinterpret_cast<lds_cu32x2*>(rs + ((ch ^ (rq & 15)) * 16));
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x = bf16_to_f32(half16(rv[e >> 1], e & 1));
+            const float v = acc[tj][ti][4 * q + e];
+            if constexpr (MODE == kApply)
+              y[e] = fmaf(g.beta, x, bf16_to_f32(pk_bf16(v, 0.f) & 0xffffu));  // bf16(B X) + a X
+            else
+              y[e] = fmaf(g.beta, x, g.alpha * v);  // c (A A^T) + b A
+          }
+          out[ti][tj][q] = u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
+        }
+    }
+  } else {
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x16_t& v = acc[tj][ti];
+          out[ti][tj][q] = u32x2_t{pk_bf16(v[4 * q], v[4 * q + 1]), pk_bf16(v[4 * q + 2], v[4 * q + 3])};
+        }
+  }
+  lds_barrier();  // all fragment and R reads are done: the LDS is free for staging
+
+  // Stage the wave's 128x128 sub-block (256-byte rows, chunk ^ swz_c(row)),
+  // then store it with 16-byte lanes, 4 rows x 256 bytes per instruction.
+  lds_u8* const W = lds + wave * SLOT;
+  const int srow = lane >> 4, sch = lane & 15;
+  auto store_stage = [&](uint16_t* dst, int ld) {
+    wait_lgkm<0>();
+#pragma unroll
+    for (int n = 0; n < 32; ++n) {
+      const int r = 4 * n + srow;
+      const u32x4_t v = *reinterpret_cast<lds_cu32x4*>(W + r * 256 + ((sch ^ swz_c(r)) * 16));
+      *reinterpret_cast<u32x4_t*>(dst + (int64_t)r * ld + sch * 8) = v;
+    }
+  };
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = 32 * ti + l32, ch = 4 * tj + q;
+        *reinterpret_cast<lds_u32x2*>(W + r * 256 + ((ch ^ swz_c(r)) * 16) + hi * 8) = out[ti][tj][q];
+      }
+  uint16_t* Ct = g.C + tile * g.c_bs;
+  store_stage(Ct + (int64_t)(bi * BT + wm * 128) * g.ldc + bj * BT + wn * 128, g.ldc);
+  if constexpr (MODE != kApply && !DIAG) {
+    // Mirror block (bj, bi): after the quad transpose, lane (a = l32/4,
+    // k = l32%4) holds C^T[jt][it..it+3], jt = 32 tj + 8 q + 4 hi + k,
+    // it = 32 ti + 4 a (wave-local).
+    wait_lgkm<0>();  // this wave's staging reads are done
+    const int k = lane & 3, a = l32 >> 2;
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x2_t tv = quad_transpose(out[ti][tj][q], k);
+          const int r = 32 * tj + 8 * q + 4 * hi + k, ch = 4 * ti + (a >> 1);
+          *reinterpret_cast<lds_u32x2*>(W + r * 256 + ((ch ^ swz_c(r)) * 16) + (a & 1) * 8) = tv;
+        }
+    store_stage(Ct + (int64_t)(bj * BT + wn * 128) * g.ldc + bi * BT + wm * 128, g.ldc);
+  }
+}
+
+// NKC: K units known at compile time (16: K = 512, the tile_size 512 case;
+// 0: K from the arguments).
+template <int MODE, int NKC>
+__global__ __launch_bounds__(NT, 1) void ns_st_kernel(StArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+  const int nbi = g.M / BT, nbj = g.N / BT;
+  const int per_tile = (MODE == kApply) ? nbi * nbj : nbi * (nbi + 1) / 2;
+  const int64_t total = g.ntiles * per_tile;
+  const int wper = (int)(gridDim.x >> 3);
+  const int64_t per_xcd = (total + 7) >> 3;
+  const int64_t ibeg = (int64_t)(blockIdx.x & 7) * per_xcd;
+  const int64_t iend = (ibeg + per_xcd < total) ? ibeg + per_xcd : total;
+  for (int64_t item = ibeg + (blockIdx.x >> 3); item < iend; item += wper) {
+    const int64_t tile = item / per_tile;
+    const int p = (int)(item - tile * per_tile);
+    if constexpr (MODE == kApply) {
+      const int bi = p / nbj;
+      st_item<MODE, false, NKC>(g, (lds_u8*)lds, tile, bi, p - bi * nbj);
+    } else {
+      int bi = 0;
+      while ((bi + 1) * (bi + 2) / 2 <= p) ++bi;
+      const int bj = p - bi * (bi + 1) / 2;
+      if (bi == bj)
+        st_item<MODE, true, NKC>(g, (lds_u8*)lds, tile, bi, bj);
+      else
+        st_item<MODE, false, NKC>(g, (lds_u8*)lds, tile, bi, bj);
+    }
+  }
+}
+
+// X0 = bf16(x * inv) in place, 8 elements per thread.
+__global__ __launch_bounds__(NT) void ns_st_scale_kernel(uint16_t* __restrict__ x,
+                                                         const float* __restrict__ inv,
+                                                         int64_t per_tile, int64_t ntiles) {
+  const int64_t nvec = ntiles * per_tile / 8;
+  for (int64_t v = (int64_t)blockIdx.x * NT + threadIdx.x; v < nvec; v += (int64_t)gridDim.x * NT) {
+    u32x4_t* p = reinterpret_cast<u32x4_t*>(x) + v;
+    *p = scale8(*p, inv[(v * 8) / per_tile]);
+  }
+}
+
+int g_num_cus[16] = {0};
+
+int num_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  const int d = dev & 15;
+  if (g_num_cus[d] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    g_num_cus[d] = n;
+  }
+  return g_num_cus[d];
+}
+
+template <int MODE>
+void launch(const StArgs& a, int64_t items, hipStream_t s) {
+  const int64_t per_xcd = (items + 7) / 8;
+  const int64_t wgs_per_xcd = std::max<int64_t>(1, std::min<int64_t>(num_cus() / 8, per_xcd));
+  const dim3 grid((unsigned)(8 * wgs_per_xcd));
+  if (a.K == 16 * BK)
+    hipLaunchKernelGGL((ns_st_kernel<MODE, 16>), grid, dim3(NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((ns_st_kernel<MODE, 0>), grid, dim3(NT), 0, s, a);
+}
+
+}  // namespace
+
+bool ns5_stream_supported(int mp, int np) { return mp % BT == 0 && np % BT == 0; }
+
+// One sub-batch of `cnt` tiles, `steps` >= 1 iterations, ping-ponging X
+// between x and y (x is scaled in place first); A and B live in the
+// workspace.
+void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
+                    float a, float b, float c, uint16_t* wsA, uint16_t* wsB, hipStream_t s) {
+  const int64_t sq = (int64_t)mp * mp, rect = (int64_t)mp * np;
+  const int nb = mp / BT;
+  const int64_t gram_items = cnt * (nb * (nb + 1) / 2);
+  const int64_t apply_items = cnt * nb * (np / BT);
+  const int64_t nvec = cnt * rect / 8;
+  hipLaunchKernelGGL(ns_st_scale_kernel, dim3((unsigned)std::min<int64_t>((nvec + NT - 1) / NT, 65536)),
+                     dim3(NT), 0, s, x, inv, rect, cnt);
+  uint16_t* cur = x;
+  uint16_t* nxt = y;
+  for (int it = 0; it < steps; ++it) {
+    const StArgs ga{cur, rect, np, cur, rect, np, nullptr, 0, 0, wsA, sq, mp, mp, mp, np, cnt, 1.0f, 0.0f};
+    launch<kGramA>(ga, gram_items, s);
+    const StArgs gb{wsA, sq, mp, wsA, sq, mp, wsA, sq, mp, wsB, sq, mp, mp, mp, mp, cnt, c, b};
+    launch<kGramB>(gb, gram_items, s);
+    const StArgs ap{wsB, sq, mp, cur, rect, np, cur, rect, np, nxt, rect, np, mp, np, mp, cnt, 1.0f, a};
+    launch<kApply>(ap, apply_items, s);
+    std::swap(cur, nxt);
+  }
+}

@@ -66,11 +66,12 @@ GATHER_CASES = [
 ]
 
 
-@pytest.fixture(params=["big", "nt", "pk", "small"])
+@pytest.fixture(params=["stream", "big", "nt", "pk", "small"])
 def ns_family(request, monkeypatch):
-    """Run a test under each NS kernel family (256-blocks, persistent NT with
-    X^T buffers, 128-blocks); shapes a family cannot take fall back to the
-    128-block kernels."""
+    """Run a test under each NS kernel family (persistent streamed-operand
+    256-blocks, 256-blocks, persistent NT with X^T buffers, persistent
+    direct-load 256-blocks, 128-blocks); shapes a family cannot take fall back
+    to the 128-block kernels."""
     monkeypatch.setenv("HIMUON_NS_PATH", request.param)
     return request.param
 
