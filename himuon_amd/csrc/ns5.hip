@@ -315,12 +315,14 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
   uint16_t* wsB = wsA + sb * sq;
   // Kernel family for tiles whose padded edges are multiples of 256: the
   // persistent streamed-operand kernels by default; HIMUON_NS_PATH =
-  // big | nt | pk | small selects another family (comparison runs; nt also
-  // needs the caller's X^T buffers). Other tiles run the 128-block kernels.
+  // t512 (512x512 tiles only) | big | nt | pk | small selects another family
+  // (comparison runs; nt also needs the caller's X^T buffers). Other tiles
+  // run the 128-block kernels.
   const char* path = getenv("HIMUON_NS_PATH");
   const char p0 = path ? path[0] : 0;
   const bool al256 = ns5_stream_supported(mp, np);
-  const bool st = al256 && (p0 == 0 || p0 == 's' && path[1] == 't');
+  const bool t5 = ns5_t512_supported(mp, np) && p0 == 't';
+  const bool st = al256 && !t5 && (p0 == 0 || p0 == 't' || (p0 == 's' && path[1] == 't'));
   const bool pk = al256 && p0 == 'p';
   const bool nt = al256 && p0 == 'n' && xt;
   const bool big = al256 && (p0 == 'b' || (p0 == 'n' && !xt));
@@ -331,7 +333,9 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
   for (int64_t s0 = 0; s0 < n_tiles; s0 += sb) {
     const int64_t cnt = std::min<int64_t>(sb, n_tiles - s0);
     const int64_t o = s0 * rect;
-    if (st) {
+    if (t5) {
+      ns5_t512_run(x + o, y + o, inv + s0, cnt, steps, a, b, c, wsA, wsB, s);
+    } else if (st) {
       ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
     } else if (pk) {
       ns5_pk_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);

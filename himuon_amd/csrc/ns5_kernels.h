@@ -48,6 +48,13 @@ bool ns5_stream_supported(int mp, int np);
 void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
                     float a, float b, float c, uint16_t* wsA, uint16_t* wsB, hipStream_t s);
 
+// Persistent 512x512-tile path (ns5_t512.hip): mp == np == 512. Scales x in
+// place (X0), then runs `steps` iterations on `cnt` tiles, ping-ponging X
+// between x and y.
+bool ns5_t512_supported(int mp, int np);
+void ns5_t512_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int steps, float a, float b, float c,
+                  uint16_t* wsA, uint16_t* wsB, hipStream_t s);
+
 // 256x256-block stages (M, N, K multiples of 256 / 64).
 void ns5_launch_gram256(const uint16_t* S, int64_t s_bs, int ldS, uint16_t* C, int64_t c_bs,
                         int ldC, const float* inv, int M, int K, int64_t ntiles, float alpha,

@@ -66,10 +66,10 @@ GATHER_CASES = [
 ]
 
 
-@pytest.fixture(params=["stream", "big", "nt", "pk", "small"])
+@pytest.fixture(params=["t512", "stream", "big", "nt", "pk", "small"])
 def ns_family(request, monkeypatch):
-    """Run a test under each NS kernel family (persistent streamed-operand
-    256-blocks, 256-blocks, persistent NT with X^T buffers, persistent
+    """Run a test under each NS kernel family (persistent 512x512-tile kernels,
+    persistent streamed-operand 256-blocks, 256-blocks, persistent NT with X^T buffers, persistent
     direct-load 256-blocks, 128-blocks); shapes a family cannot take fall back
     to the 128-block kernels."""
     monkeypatch.setenv("HIMUON_NS_PATH", request.param)
@@ -272,3 +272,32 @@ def test_ns5_workspace_too_small_raises():
     ws = torch.empty(16, device=DEV, dtype=torch.uint8)
     with pytest.raises(RuntimeError, match="workspace"):
         grp.ns(0, 2, 5, ws, 2)
+
+
+def test_ns5_t512_many_tiles_large_buffers():
+    """4096 tiles of 512x512: tile buffers of 2 GiB (addresses with bit 31 of
+    the low word set, as for real models), persistent workgroups that run many
+    output blocks each (cross-block operand prefetch and deferred stores).
+    Sampled tiles match the reference's same-dtype NS5; the result does not
+    depend on the sub-batch size (bitwise)."""
+    n, T = 4096, 512
+    print(f"[ns5 t512 large] n={n}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    G = (torch.randn((n, T, T), generator=gen, device=DEV) * 1e-3).to(torch.bfloat16)
+    flat = G.view(-1, T)
+    grp = TileGroup([flat], [flat], [None], T, T, [1.0], [0.0], [False], torch.device(DEV), torch.bfloat16)
+    outs = []
+    for sb in (n, 1000):
+        grp.gather()
+        ws = torch.empty(grp.workspace_bytes(sb), device=DEV, dtype=torch.uint8)
+        grp.ns(0, grp.n_tiles, 5, ws, sb)
+        outs.append(grp.result(5).clone())
+        del ws
+    assert torch.equal(outs[0], outs[1])
+    out = outs[0]
+    assert torch.isfinite(out.float()).all()
+    idx = torch.tensor([0, 1, 2, 1023, 2048, 2049, 3071, 4095], device=DEV)
+    ref = ns5_torch_staged(G[idx])
+    err = per_tile_rel_fro(out[idx].float(), ref.float())
+    print(f"  sampled tiles vs staged torch: max {err.max():.4f} mean {err.mean():.4f}", flush=True)
+    assert err.mean() <= 1e-2 and err.max() <= 2e-2
