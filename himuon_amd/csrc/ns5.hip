@@ -284,9 +284,14 @@ __global__ __launch_bounds__(kThreads) void ns_scale_copy_kernel(const uint16_t*
 
 }  // namespace
 
+// A and B per sub-batch tile, then the dataflow counters (256-byte aligned).
+size_t ws_ab_bytes(int64_t sub_batch, int mp) {
+  return (2 * (size_t)sub_batch * mp * mp * sizeof(uint16_t) + 255) & ~(size_t)255;
+}
+
 extern "C" size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np) {
   if (sub_batch <= 0 || mp <= 0 || np <= 0) return 0;
-  return 2 * (size_t)sub_batch * mp * mp * sizeof(uint16_t);  // A and B per sub-batch tile
+  return ws_ab_bytes(sub_batch, mp) + ns5_flow_counter_bytes(sub_batch);
 }
 
 extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, const float* inv,
@@ -314,15 +319,19 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
   uint16_t* wsA = static_cast<uint16_t*>(workspace);
   uint16_t* wsB = wsA + sb * sq;
   // Kernel family for tiles whose padded edges are multiples of 256: the
-  // persistent streamed-operand kernels by default; HIMUON_NS_PATH =
-  // t512 (512x512 tiles only) | big | nt | pk | small selects another family
-  // (comparison runs; nt also needs the caller's X^T buffers). Other tiles
-  // run the 128-block kernels.
+  // persistent two-workgroups-per-CU kernels by default; HIMUON_NS_PATH =
+  // stream | t512 (512x512 tiles only) | big | nt | pk | small selects another
+  // family (comparison runs; nt also needs the caller's X^T buffers). Other
+  // tiles run the 128-block kernels.
   const char* path = getenv("HIMUON_NS_PATH");
   const char p0 = path ? path[0] : 0;
   const bool al256 = ns5_stream_supported(mp, np);
+  const bool duo = al256 && ns5_duo_supported(mp, np) && (p0 == 0 || p0 == 'd' || p0 == 'f');
+  const bool flow = duo && p0 == 'f';
+  const char* wenv = getenv("HIMUON_NS_WINDOW");
+  const int window = wenv ? atoi(wenv) : 16;
   const bool t5 = ns5_t512_supported(mp, np) && p0 == 't';
-  const bool st = al256 && !t5 && (p0 == 0 || p0 == 't' || (p0 == 's' && path[1] == 't'));
+  const bool st = al256 && !t5 && (p0 == 't' || (p0 == 's' && path[1] == 't'));
   const bool pk = al256 && p0 == 'p';
   const bool nt = al256 && p0 == 'n' && xt;
   const bool big = al256 && (p0 == 'b' || (p0 == 'n' && !xt));
@@ -333,7 +342,12 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
   for (int64_t s0 = 0; s0 < n_tiles; s0 += sb) {
     const int64_t cnt = std::min<int64_t>(sb, n_tiles - s0);
     const int64_t o = s0 * rect;
-    if (t5) {
+    if (flow) {
+      int* counters = reinterpret_cast<int*>(static_cast<uint8_t*>(workspace) + ws_ab_bytes(sb, mp));
+      ns5_flow_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, counters, window, s);
+    } else if (duo) {
+      ns5_duo_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
+    } else if (t5) {
       ns5_t512_run(x + o, y + o, inv + s0, cnt, steps, a, b, c, wsA, wsB, s);
     } else if (st) {
       ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);

@@ -48,6 +48,21 @@ bool ns5_stream_supported(int mp, int np);
 void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
                     float a, float b, float c, uint16_t* wsA, uint16_t* wsB, hipStream_t s);
 
+// Persistent two-workgroups-per-CU path (ns5_duo.hip): mp a multiple of 256,
+// np of 128. Scales x in place (X0), then runs `steps` iterations on `cnt`
+// tiles, ping-ponging X between x and y.
+bool ns5_duo_supported(int mp, int np);
+void ns5_duo_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
+                 float a, float b, float c, uint16_t* wsA, uint16_t* wsB, hipStream_t s);
+
+// Dataflow variant of the same kernels (ns5_duo.hip): one persistent launch
+// for all iterations; windows of `window` tiles are processed XCD-locally.
+// `counters` is the workspace tail of ns5_flow_counter_bytes(cnt) bytes.
+size_t ns5_flow_counter_bytes(int64_t cnt);
+void ns5_flow_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
+                  float a, float b, float c, uint16_t* wsA, uint16_t* wsB, int* counters, int window,
+                  hipStream_t s);
+
 // Persistent 512x512-tile path (ns5_t512.hip): mp == np == 512. Scales x in
 // place (X0), then runs `steps` iterations on `cnt` tiles, ping-ponging X
 // between x and y.

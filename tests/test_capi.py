@@ -64,7 +64,12 @@ def test_partials_per_tile(lib):
 
 
 def test_workspace_bytes(lib):
-    assert lib.himuon_ns5_workspace_bytes(4, 512, 512) == 2 * 4 * 512 * 512 * 2  # A and B
+    # A and B per sub-batch tile (256-byte aligned), then the dataflow counters:
+    # prog[n], 32 ints of queue state, wseq[16][n + 1].
+    n = 4
+    ab = 2 * n * 512 * 512 * 2
+    assert lib.himuon_ns5_workspace_bytes(n, 512, 512) == ab + 4 * (n + 32 + 16 * (n + 1))
+    assert lib.himuon_ns5_workspace_bytes(3, 128, 256) == ((2 * 3 * 128 * 128 * 2 + 255) // 256) * 256 + 4 * (3 + 32 + 16 * 4)
     assert lib.himuon_ns5_workspace_bytes(0, 512, 512) == 0
 
 

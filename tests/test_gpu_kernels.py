@@ -66,9 +66,10 @@ GATHER_CASES = [
 ]
 
 
-@pytest.fixture(params=["t512", "stream", "big", "nt", "pk", "small"])
+@pytest.fixture(params=["flow", "duo", "t512", "stream", "big", "nt", "pk", "small"])
 def ns_family(request, monkeypatch):
-    """Run a test under each NS kernel family (persistent 512x512-tile kernels,
+    """Run a test under each NS kernel family (dataflow two-workgroups-per-CU
+    kernel, persistent two-workgroups-per-CU kernels, persistent 512x512-tile kernels,
     persistent streamed-operand 256-blocks, 256-blocks, persistent NT with X^T buffers, persistent
     direct-load 256-blocks, 128-blocks); shapes a family cannot take fall back
     to the 128-block kernels."""
