@@ -52,6 +52,23 @@ class ParamDesc(ctypes.Structure):
 
 assert ctypes.sizeof(ParamDesc) == 96
 
+
+class ApplyDesc(ctypes.Structure):
+    """Mirror of HimuonApplyDesc (include/himuon_hip.h)."""
+
+    _fields_ = [
+        ("param", c_void_p),
+        ("update", c_void_p),
+        ("numel", c_int64),
+        ("chunk0", c_int64),
+        ("group", c_int32),
+        ("reserved", c_int32),
+    ]
+
+
+assert ctypes.sizeof(ApplyDesc) == 40
+APPLY_MAX_GROUPS = 32
+
 # name -> (restype, argtypes)
 _SIGNATURES = {
     "himuon_abi_version": (c_int, []),
@@ -88,6 +105,12 @@ _SIGNATURES = {
     "himuon_untile": (
         c_int,
         [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p],
+    ),
+    "himuon_apply_chunk_elems": (c_int64, []),
+    "himuon_apply_updates": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int, c_int, ctypes.POINTER(c_float), ctypes.POINTER(c_float), c_int,
+         c_void_p],
     ),
 }
 
@@ -289,3 +312,24 @@ def lr_scale(block_shape, lr_adjust: str = "tile") -> float:
         return 1.0
     a, b = block_shape[:2]
     return 0.2 * math.sqrt(max(a, b))
+
+
+def apply_updates(desc_table, n_descs, n_chunks, param_dtype, update_dtype, scales, alphas):
+    """One launch of the WD + LR application over a descriptor table
+    (himuon.py:215-228); scales/alphas are per-group host floats."""
+    n = len(scales)
+    s_arr = (c_float * n)(*scales)
+    a_arr = (c_float * n)(*alphas)
+    _check(
+        load().himuon_apply_updates(
+            desc_table.data_ptr(), n_descs, n_chunks, DTYPE_CODES[param_dtype], DTYPE_CODES[update_dtype],
+            s_arr, a_arr, n, _stream(),
+        ),
+        "himuon_apply_updates",
+    )
+
+
+def apply_desc_table(descs: list[ApplyDesc], device) -> torch.Tensor:
+    arr = (ApplyDesc * len(descs))(*descs)
+    host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
+    return host.to(device)

@@ -319,19 +319,19 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
   uint16_t* wsA = static_cast<uint16_t*>(workspace);
   uint16_t* wsB = wsA + sb * sq;
   // Kernel family for tiles whose padded edges are multiples of 256: the
-  // persistent two-workgroups-per-CU kernels by default; HIMUON_NS_PATH =
-  // stream | t512 (512x512 tiles only) | big | nt | pk | small selects another
+  // persistent streamed-operand kernels by default; HIMUON_NS_PATH = duo |
+  // flow | t512 (512x512 tiles only) | big | nt | pk | small selects another
   // family (comparison runs; nt also needs the caller's X^T buffers). Other
   // tiles run the 128-block kernels.
   const char* path = getenv("HIMUON_NS_PATH");
   const char p0 = path ? path[0] : 0;
   const bool al256 = ns5_stream_supported(mp, np);
-  const bool duo = al256 && ns5_duo_supported(mp, np) && (p0 == 0 || p0 == 'd' || p0 == 'f');
+  const bool duo = al256 && ns5_duo_supported(mp, np) && (p0 == 'd' || p0 == 'f');
   const bool flow = duo && p0 == 'f';
   const char* wenv = getenv("HIMUON_NS_WINDOW");
   const int window = wenv ? atoi(wenv) : 16;
   const bool t5 = ns5_t512_supported(mp, np) && p0 == 't';
-  const bool st = al256 && !t5 && (p0 == 't' || (p0 == 's' && path[1] == 't'));
+  const bool st = al256 && !t5 && !duo && (p0 == 0 || p0 == 't' || (p0 == 's' && path[1] == 't'));
   const bool pk = al256 && p0 == 'p';
   const bool nt = al256 && p0 == 'n' && xt;
   const bool big = al256 && (p0 == 'b' || (p0 == 'n' && !xt));

@@ -19,56 +19,6 @@ struct Geo {
   int tile_h, tile_w, mp, np;
 };
 
-// 8 consecutive elements of a gradient-typed row, as fp32.
-template <int DT>
-HM_DEV void load8(const void* base, int64_t off, float v[8]) {
-  if constexpr (DT == HIMUON_DTYPE_F32) {
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
-    const float4 a = p[0], b = p[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      if constexpr (DT == HIMUON_DTYPE_BF16) {
-        v[2 * k] = bf16_to_f32(w[k] & 0xffffu);
-        v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-      } else {
-        v[2 * k] = f16_to_f32((uint16_t)(w[k] & 0xffffu));
-        v[2 * k + 1] = f16_to_f32((uint16_t)(w[k] >> 16));
-      }
-    }
-  }
-}
-
-template <int DT>
-HM_DEV void store8(void* base, int64_t off, const float v[8]) {
-  if constexpr (DT == HIMUON_DTYPE_F32) {
-    float4* p = reinterpret_cast<float4*>(static_cast<float*>(base) + off);
-    p[0] = make_float4(v[0], v[1], v[2], v[3]);
-    p[1] = make_float4(v[4], v[5], v[6], v[7]);
-  } else {
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      if constexpr (DT == HIMUON_DTYPE_BF16) {
-        w[k] = pack2(f32_to_bf16(v[2 * k]), f32_to_bf16(v[2 * k + 1]));
-      } else {
-        w[k] = pack2(f32_to_f16(v[2 * k]), f32_to_f16(v[2 * k + 1]));
-      }
-    }
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + off) = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-}
-
-template <int DT>
-HM_DEV bool aligned16(const void* base, int64_t off) {
-  constexpr int es = (DT == HIMUON_DTYPE_F32) ? 4 : 2;
-  return ((reinterpret_cast<uintptr_t>(base) + (uintptr_t)off * es) & 15u) == 0;
-}
-
 // Momentum for one element (himuon.py:354-356); returns the NS input and
 // writes the new momentum value to *m. Results are rounded to the tensor
 // dtype where torch stores them: buf.mul_(mu) and .add_(g) each store (two

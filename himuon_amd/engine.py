@@ -147,6 +147,44 @@ class TileGroup:
         return nat.default_sub_batch(self.n_tiles, self.mp, self.np)
 
 
+class ApplyTables:
+    """Device descriptor tables for the WD + LR application of a list of
+    (param, update, group_idx), one table per (param dtype, update dtype)
+    pair, built once (pointers must stay put: the graph path's updates and
+    the parameters do). Entries the kernel cannot take (non-contiguous,
+    misaligned, other dtypes, more than APPLY_MAX_GROUPS groups) are left to
+    the torch ops of the reference (``fallback``)."""
+
+    def __init__(self, entries):
+        chunk = int(nat.load().himuon_apply_chunk_elems())
+        by_pair: dict[tuple, list] = {}
+        self.fallback = []
+        for p, u, gi in entries:
+            pd, ud = p.data, u
+            ok = (
+                pd.is_cuda and ud.is_cuda and pd.is_contiguous() and ud.is_contiguous()
+                and pd.numel() == ud.numel() and pd.dtype in nat.DTYPE_CODES and ud.dtype in nat.DTYPE_CODES
+                and pd.data_ptr() % 16 == 0 and ud.data_ptr() % 16 == 0 and gi < nat.APPLY_MAX_GROUPS
+            )
+            if ok:
+                by_pair.setdefault((pd.dtype, ud.dtype), []).append((pd, ud, gi))
+            else:
+                self.fallback.append((p, u, gi))
+        self.launches = []  # (table, n_descs, n_chunks, pdtype, udtype)
+        for (pdt, udt), lst in by_pair.items():
+            descs, c0 = [], 0
+            for pd, ud, gi in lst:
+                d = nat.ApplyDesc()
+                d.param, d.update, d.numel, d.chunk0, d.group = pd.data_ptr(), ud.data_ptr(), pd.numel(), c0, gi
+                descs.append(d)
+                c0 += -(-pd.numel() // chunk)
+            self.launches.append((nat.apply_desc_table(descs, lst[0][0].device), len(descs), c0, pdt, udt))
+
+    def run(self, scales: list[float], alphas: list[float]) -> None:
+        for table, n, n_chunks, pdt, udt in self.launches:
+            nat.apply_updates(table, n, n_chunks, pdt, udt, scales, alphas)
+
+
 def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     """Batched NS5 of ``G`` (..., M, N) on the HIP path; same shape and dtype.
 

@@ -29,7 +29,7 @@ import torch
 from torch.optim import Optimizer
 
 from .. import _native as nat
-from ..engine import TileGroup
+from ..engine import ApplyTables, TileGroup
 from ..engine import newton_schulz as _hip_newton_schulz
 
 try:
@@ -102,6 +102,7 @@ class HiMuon(Optimizer):
         self._in_graph_region: bool = False
         # (param, update_tensor, group_idx), filled at capture, applied after replay.
         self._pending_updates: list[tuple] = []
+        self._apply_tables: "ApplyTables | None" = None  # device tables for _pending_updates
 
         # Device state of the HIP path, rebuilt after reconfigure().
         self._groups: "list[dict] | None" = None  # tiled buckets + full-NS shape groups
@@ -151,10 +152,23 @@ class HiMuon(Optimizer):
         self._cuda_graph = None
         self._graph_step_count = 0
         self._pending_updates.clear()
+        self._apply_tables = None
 
     def _apply_pending_updates(self):
-        """WD + LR application after replay, reading the current group lr/wd."""
-        for p, update, group_idx in self._pending_updates:
+        """WD + LR application after replay, reading the current group lr/wd:
+        one multi-tensor HIP launch per dtype pair (himuon_apply_updates) with
+        lr/wd passed as host scalars, so schedules need no recapture."""
+        if not self._pending_updates:
+            return
+        if self._apply_tables is None:
+            self._apply_tables = ApplyTables(self._pending_updates)
+        scales, alphas = [], []
+        for group in self.param_groups:
+            lr, weight_decay = group["lr"], group["weight_decay"]
+            scales.append(1 - lr * weight_decay if weight_decay > 0.0 else 1.0)
+            alphas.append(-lr)
+        self._apply_tables.run(scales, alphas)
+        for p, update, group_idx in self._apply_tables.fallback:
             group = self.param_groups[group_idx]
             lr = group["lr"]
             weight_decay = group["weight_decay"]
@@ -502,6 +516,7 @@ class HiMuon(Optimizer):
         self._ensure_device_state()  # allocate everything before capture
         torch.cuda.synchronize()
         self._pending_updates.clear()
+        self._apply_tables = None
         self._cuda_graph = torch.cuda.CUDAGraph()
         self._in_graph_region = True
         try:

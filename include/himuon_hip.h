@@ -158,6 +158,39 @@ int himuon_untile(const HimuonParamDesc* params_dev, int n_params,
                   int64_t n_tiles, int tile_h, int tile_w, int mp, int np,
                   int dtype, const uint16_t* tiles_bf16, void* stream);
 
+/*
+ * Weight decay + learning-rate application, outside the captured graph
+ * (replaces _apply_pending_updates, himuon.py:215-228, and the eager
+ * _apply_wd_and_update, himuon.py:333-348). One descriptor per parameter, in
+ * device memory, built once per capture; each parameter's elements are cut
+ * into chunks of himuon_apply_chunk_elems() and descriptor d owns chunks
+ * [chunk0_d, chunk0_d + ceil(numel_d / chunk)) of the launch. param and
+ * update must be contiguous and 16-byte aligned. For every element:
+ *     p1 = round_p(float(p) * scale[group]);          p.mul_(1 - lr*wd)
+ *     p  = round_p(fma(alpha[group], round_p(u), p1)) p.add_(u, alpha=-lr)
+ * scale_by_group / alpha_by_group are HOST arrays of n_groups floats (copied
+ * into the launch), so lr and wd may change every step without re-recording.
+ * One launch covers the descriptors of one (param dtype, update dtype) pair.
+ */
+#define HIMUON_APPLY_MAX_GROUPS 32
+
+typedef struct HimuonApplyDesc {
+  void* param;         /* contiguous parameter                          */
+  const void* update;  /* contiguous update, same number of elements    */
+  int64_t numel;
+  int64_t chunk0;      /* first chunk of this parameter in the launch    */
+  int32_t group;       /* index into scale_by_group / alpha_by_group     */
+  int32_t reserved;
+} HimuonApplyDesc;
+
+int64_t himuon_apply_chunk_elems(void);
+
+int himuon_apply_updates(const HimuonApplyDesc* descs_dev, int n_descs,
+                         int64_t n_chunks, int param_dtype, int update_dtype,
+                         const float* scale_by_group,
+                         const float* alpha_by_group, int n_groups,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -329,12 +329,15 @@ def lr_scale(block_shape, lr_adjust: str = "tile") -> float:
 
 
 def apply_update(p, update, lr: float, wd: float, dtype: str = "float32") -> np.ndarray:
-    """p <- p * (1 - lr*wd) (if wd > 0); p <- p - lr * update, each stored in
-    the parameter dtype (himuon.py:222-228)."""
+    """p.mul_(1 - lr*wd) (if wd > 0), then p.add_(update, alpha=-lr), each
+    stored in the parameter dtype (himuon.py:222-228, 345-348). torch's
+    in-place add computes in the parameter's dtype: the update is first
+    rounded to it, then `p + alpha * u` is one fp32 fused multiply-add."""
     p = np.asarray(p, dtype=F32)
     if wd > 0.0:
         p = round_to(p * F32(1 - lr * wd), dtype)
-    return round_to(p + F32(-lr) * np.asarray(update, dtype=F32), dtype)
+    u = round_to(np.asarray(update, dtype=F32), dtype)
+    return round_to(fma32(F32(-lr), u, p), dtype)
 
 
 @dataclass

@@ -73,6 +73,43 @@ def test_momentum_matches_torch_inplace_ops(dtype):
         assert np.array_equal(ge.view(np.uint32), O.bf16_round(O.fma32(np.float32(0.95), b1, g)).view(np.uint32))
 
 
+# ---------------------------------------------------------------------------
+# Weight decay + LR application (himuon.py:215-228, 345-348)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("udt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("lr,wd", [(1e-2, 0.1), (3e-3, 0.0)])
+def test_apply_update_fp32_matches_torch_ops(udt, lr, wd):
+    """fp32 parameters: p.mul_(1 - lr*wd); p.add_(u, alpha=-lr) on torch's CPU
+    kernels equals the oracle bit for bit (the fused multiply-add; an unfused
+    p + (alpha*u) differs on this sample). bf16/fp16 parameters are pinned
+    against torch on the GPU (tests/test_gpu_apply.py): torch's CPU kernels
+    round low-precision adds differently from its GPU kernels."""
+    rng = np.random.default_rng(5)
+    p = torch.from_numpy((rng.standard_normal(50001) * 0.02).astype(np.float32))
+    u = torch.from_numpy((rng.standard_normal(50001) * 0.5).astype(np.float32)).to(udt)
+    ref = p.clone()
+    if wd > 0:
+        ref.mul_(1 - lr * wd)
+    ref.add_(u, alpha=-lr)
+    got = O.apply_update(p.numpy(), u.float().numpy(), lr, wd, "float32")
+    assert np.array_equal(got.view(np.uint32), ref.numpy().view(np.uint32))
+    p1 = p.numpy() * np.float32(1 - lr * wd) if wd > 0 else p.numpy()
+    unfused = (p1 + np.float32(-lr) * u.float().numpy()).astype(np.float32)
+    assert not np.array_equal(unfused, ref.numpy())
+
+
+@pytest.mark.parametrize("dtype,tdt", [("bfloat16", torch.bfloat16), ("float16", torch.float16)])
+def test_apply_update_weight_decay_matches_torch_mul(dtype, tdt):
+    """The decay stage p.mul_(1 - lr*wd) of low-precision parameters (one fp32
+    product rounded to the parameter dtype) equals torch's CPU kernel."""
+    rng = np.random.default_rng(6)
+    p = torch.from_numpy((rng.standard_normal(50001) * 0.02).astype(np.float32)).to(tdt)
+    ref = p.clone().mul_(1 - 1e-2 * 0.1)
+    # with a zero update the add stage is the identity
+    got = O.apply_update(p.float().numpy(), np.zeros(50001, np.float32), 1e-2, 0.1, dtype)
+    assert np.array_equal(got, ref.float().numpy())
+
+
 def test_fma32_is_correctly_rounded():
     """fma32 against exact rational arithmetic, including cancellation and
     halfway cases that a float64 evaluation would double-round."""
