@@ -36,10 +36,7 @@ PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 4096 FLOP/clk x 2.
 
 # NS stage kernels per kernel family (HIMUON_NS_PATH), per NS iteration.
 NS_KERNELS = {
-    "t512": "ns5 stage: ns_t512_kernel<0> (X X^T), <1> (c A A^T + b A), <2> (B X + a X) per iteration",
     "stream": "ns5 stage: ns_st_kernel<0> (X X^T), <1> (c A A^T + b A), <2> (B X + a X) per iteration",
-    "big": "ns5 stage: ns_gram256_kernel x2 + ns_apply256_kernel per iteration",
-    "nt": "ns5 stage: ns_nt_kernel (gram A, gram B, apply) per iteration",
     "small": "ns5 stage: ns_gram_kernel x2 + ns_apply_kernel per iteration",
 }
 

@@ -19,7 +19,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libhimuon_hip.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 NS_ALIGN = 128
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -76,16 +76,13 @@ _SIGNATURES = {
     "himuon_gather_partials_per_tile": (c_int, [c_int, c_int, c_int, c_int]),
     "himuon_momentum_gather": (
         c_int,
-        [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
-         c_void_p],
+        [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p],
     ),
     "himuon_tile_scale": (c_int, [c_void_p, c_int, c_int64, c_float, c_void_p, c_void_p]),
     "himuon_ns5_workspace_bytes": (c_size_t, [c_int64, c_int, c_int]),
     "himuon_ns5": (
         c_int,
         [
-            c_void_p,
-            c_void_p,
             c_void_p,
             c_void_p,
             c_void_p,
@@ -196,16 +193,8 @@ def ns5_workspace_bytes(sub_batch: int, mp: int, np_: int) -> int:
 
 def ns_path() -> str:
     """NS kernel family for 256-aligned tiles: HIMUON_NS_PATH = "stream"
-    (persistent streamed-operand kernels, the default), "big", "pk", "nt"
-    (persistent kernel reading X and X^T) or "small" (128-blocks)."""
+    (persistent streamed-operand kernels, the default) or "small" (128-blocks)."""
     return os.environ.get("HIMUON_NS_PATH", "stream")
-
-
-def nt_path(mp: int, np_: int) -> bool:
-    """True when the NS stage runs the persistent NT kernel, which also needs
-    the transposed X buffers: both padded edges multiples of 256 and the
-    "nt" family selected."""
-    return ns_path() == "nt" and mp % 256 == 0 and np_ % 256 == 0
 
 
 def default_sub_batch(n_tiles: int, mp: int, np_: int) -> int:
@@ -232,7 +221,7 @@ def make_desc_table(descs: list[ParamDesc], device) -> torch.Tensor:
 # ---------------------------------------------------------------------------
 # Entry points
 # ---------------------------------------------------------------------------
-def momentum_gather(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtype, tiles, tiles_t, partials):
+def momentum_gather(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtype, tiles, partials):
     _check(
         load().himuon_momentum_gather(
             desc_table.data_ptr(),
@@ -244,7 +233,6 @@ def momentum_gather(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtyp
             np_,
             dtype_code(dtype),
             tiles.data_ptr(),
-            _ptr(tiles_t),
             partials.data_ptr(),
             _stream(),
         ),
@@ -259,18 +247,16 @@ def tile_scale(partials, per_tile, n_tiles, inv, eps=NS_EPS):
     )
 
 
-def ns5(x, xt, y, yt, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, NS_B, NS_C)):
-    """NS5 on tiles x (and x^T in xt); X ping-pongs into y: the result is in x
-    for an even step count and in y for an odd one."""
+def ns5(x, y, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, NS_B, NS_C)):
+    """NS5 on tiles x; X ping-pongs into y: the result is in x for an even
+    step count and in y for an odd one."""
     a, b, c = coeffs
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check(
         load().himuon_ns5(
             x.data_ptr(),
-            _ptr(xt),
             y.data_ptr(),
-            _ptr(yt),
             inv.data_ptr(),
             n_tiles,
             mp,

@@ -14,14 +14,16 @@
 //
 // HBM-bound: read p, read u, write p (8 B per element for bf16 params and
 // fp32 updates, against 12 B for the two separate torch passes). Work is cut
-// into chunks of 4096 elements per parameter; a persistent grid walks the
-// chunks, each thread handling two 8-element vectors.
+// into chunks of 8192 elements per parameter; a persistent grid walks the
+// chunks, each thread issuing the loads of its four 8-element vectors before
+// using them.
 #include "common.h"
 
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kChunk = 4096;  // elements per chunk: 256 threads x 2 x 8
+constexpr int kVec = 4;       // 8-element vectors per thread per chunk
+constexpr int kChunk = kThreads * kVec * 8;  // 8192 elements
 
 struct ApplyScalars {
   float s[HIMUON_APPLY_MAX_GROUPS];
@@ -47,17 +49,24 @@ __global__ __launch_bounds__(kThreads) void apply_kernel(const HimuonApplyDesc* 
     const HimuonApplyDesc& D = descs[find_desc(descs, n_descs, q)];
     const float s = sc.s[D.group], alpha = sc.alpha[D.group];
     const int64_t base = (q - D.chunk0) * kChunk;
+    float p[kVec][8], u[kVec][8];
+    // Every load of the chunk is issued before any is used.
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < kVec; ++h) {
+      const int64_t e0 = base + (int64_t)(h * kThreads + threadIdx.x) * 8;
+      if (e0 + 8 <= D.numel) {
+        load8<PD>(D.param, e0, p[h]);
+        load8<UD>(D.update, e0, u[h]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < kVec; ++h) {
       const int64_t e0 = base + (int64_t)(h * kThreads + threadIdx.x) * 8;
       if (e0 >= D.numel) continue;
       if (e0 + 8 <= D.numel) {
-        float p[8], u[8];
-        load8<PD>(D.param, e0, p);
-        load8<UD>(D.update, e0, u);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) p[e] = __builtin_fmaf(alpha, round_to<PD>(u[e]), round_to<PD>(p[e] * s));
-        store8<PD>(D.param, e0, p);
+        for (int e = 0; e < 8; ++e) p[h][e] = __builtin_fmaf(alpha, round_to<PD>(u[h][e]), round_to<PD>(p[h][e] * s));
+        store8<PD>(D.param, e0, p[h]);
       } else {
         for (int64_t e = e0; e < D.numel; ++e) {
           const float p1 = round_to<PD>(load_elem<PD>(D.param, e) * s);

@@ -284,22 +284,16 @@ __global__ __launch_bounds__(kThreads) void ns_scale_copy_kernel(const uint16_t*
 
 }  // namespace
 
-// A and B per sub-batch tile, then the dataflow counters (256-byte aligned).
-size_t ws_ab_bytes(int64_t sub_batch, int mp) {
-  return (2 * (size_t)sub_batch * mp * mp * sizeof(uint16_t) + 255) & ~(size_t)255;
-}
-
 extern "C" size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np) {
   if (sub_batch <= 0 || mp <= 0 || np <= 0) return 0;
-  return ws_ab_bytes(sub_batch, mp) + ns5_flow_counter_bytes(sub_batch);
+  return 2 * (size_t)sub_batch * mp * mp * sizeof(uint16_t);  // A and B per sub-batch tile
 }
 
-extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, const float* inv,
-                          int64_t n_tiles, int mp, int np, int steps, float a, float b, float c,
-                          void* workspace, size_t workspace_bytes, int64_t sub_batch,
-                          void* stream) {
+extern "C" int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp,
+                          int np, int steps, float a, float b, float c, void* workspace,
+                          size_t workspace_bytes, int64_t sub_batch, void* stream) {
   if (!x || !y || x == y || !inv || n_tiles < 0 || steps < 0 || mp <= 0 || np <= 0 || mp > np ||
-      mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN || sub_batch <= 0 || (xt == nullptr) != (yt == nullptr))
+      mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN || sub_batch <= 0)
     return HIMUON_EINVAL;
   if (n_tiles == 0) return 0;
   const int64_t sb = sub_batch < n_tiles ? sub_batch : n_tiles;
@@ -318,23 +312,12 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
 
   uint16_t* wsA = static_cast<uint16_t*>(workspace);
   uint16_t* wsB = wsA + sb * sq;
-  // Kernel family for tiles whose padded edges are multiples of 256: the
-  // persistent streamed-operand kernels by default; HIMUON_NS_PATH = duo |
-  // flow | t512 (512x512 tiles only) | big | nt | pk | small selects another
-  // family (comparison runs; nt also needs the caller's X^T buffers). Other
-  // tiles run the 128-block kernels.
+  // Tiles whose padded edges are multiples of 256 run the persistent
+  // streamed-operand kernels (ns5_stream.hip); HIMUON_NS_PATH=small selects the
+  // 128-block kernels below for them too (comparison runs). Other tiles always
+  // run the 128-block kernels.
   const char* path = getenv("HIMUON_NS_PATH");
-  const char p0 = path ? path[0] : 0;
-  const bool al256 = ns5_stream_supported(mp, np);
-  const bool duo = al256 && ns5_duo_supported(mp, np) && (p0 == 'd' || p0 == 'f');
-  const bool flow = duo && p0 == 'f';
-  const char* wenv = getenv("HIMUON_NS_WINDOW");
-  const int window = wenv ? atoi(wenv) : 16;
-  const bool t5 = ns5_t512_supported(mp, np) && p0 == 't';
-  const bool st = al256 && !t5 && !duo && (p0 == 0 || p0 == 't' || (p0 == 's' && path[1] == 't'));
-  const bool pk = al256 && p0 == 'p';
-  const bool nt = al256 && p0 == 'n' && xt;
-  const bool big = al256 && (p0 == 'b' || (p0 == 'n' && !xt));
+  const bool st = ns5_stream_supported(mp, np) && !(path && path[0] == 's' && path[1] == 'm');
   const int nb = mp / BM;
   const int npairs = nb * (nb + 1) / 2;
   const int apply_blocks = (mp / BM) * (np / BN);
@@ -342,39 +325,22 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt, 
   for (int64_t s0 = 0; s0 < n_tiles; s0 += sb) {
     const int64_t cnt = std::min<int64_t>(sb, n_tiles - s0);
     const int64_t o = s0 * rect;
-    if (flow) {
-      int* counters = reinterpret_cast<int*>(static_cast<uint8_t*>(workspace) + ws_ab_bytes(sb, mp));
-      ns5_flow_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, counters, window, s);
-    } else if (duo) {
-      ns5_duo_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
-    } else if (t5) {
-      ns5_t512_run(x + o, y + o, inv + s0, cnt, steps, a, b, c, wsA, wsB, s);
-    } else if (st) {
+    if (st) {
       ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
-    } else if (pk) {
-      ns5_pk_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
-    } else if (nt) {
-      ns5_nt_run(x + o, xt + o, y + o, yt + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
     } else {
       const uint16_t* cur = x + o;
       uint16_t* nxt = y + o;
       const float* cur_inv = inv + s0;
       for (int it = 0; it < steps; ++it) {
-        if (big) {
-          ns5_launch_gram256(cur, rect, np, wsA, sq, mp, cur_inv, mp, np, cnt, 1.0f, 0.0f, s);
-          ns5_launch_gram256(wsA, sq, mp, wsB, sq, mp, nullptr, mp, mp, cnt, c, b, s);
-          ns5_launch_apply256(wsB, sq, cur, rect, nxt, rect, cur_inv, mp, np, cnt, a, s);
-        } else {
-          hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(cnt * npairs)),
-                             dim3(kThreads), 0, s, cur, rect, np, wsA, sq, mp, cur_inv, mp, np,
-                             cnt, 1.0f, 0.0f);
-          hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(cnt * npairs)),
-                             dim3(kThreads), 0, s, wsA, sq, mp, wsB, sq, mp, nullptr, mp, mp, cnt,
-                             c, b);
-          hipLaunchKernelGGL(ns_apply_kernel, dim3((unsigned)xcd_grid(cnt * apply_blocks)),
-                             dim3(kThreads), 0, s, wsB, sq, cur, rect, nxt, rect, cur_inv, mp, np,
-                             cnt, a);
-        }
+        hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(cnt * npairs)),
+                           dim3(kThreads), 0, s, cur, rect, np, wsA, sq, mp, cur_inv, mp, np,
+                           cnt, 1.0f, 0.0f);
+        hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(cnt * npairs)),
+                           dim3(kThreads), 0, s, wsA, sq, mp, wsB, sq, mp, nullptr, mp, mp, cnt,
+                           c, b);
+        hipLaunchKernelGGL(ns_apply_kernel, dim3((unsigned)xcd_grid(cnt * apply_blocks)),
+                           dim3(kThreads), 0, s, wsB, sq, cur, rect, nxt, rect, cur_inv, mp, np,
+                           cnt, a);
         const uint16_t* t = cur;
         cur = nxt;
         nxt = const_cast<uint16_t*>(t);

@@ -6,13 +6,19 @@
 //   * untile: NS tile buffer -> per-parameter update (himuon.py:315-329).
 // All are HBM-bound: each element is read/written once (14 B/el for fp32
 // gather, 6 B/el for fp32 untile), with 16-byte accesses on both sides.
+// Plain tiles (tile_h <= tile_w) move whole NS rows: a work item is a slab of
+// kRows rows of one tile, walked by a persistent grid, and each thread issues
+// the loads of kVec 8-element vectors before using any of them, so enough
+// bytes are in flight to cover the memory latency. Tall tiles are transposed
+// through LDS in 64 x 64 blocks.
 #include "common.h"
 
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kSlabRows = 32;  // NS rows per gather/untile work item (plain tiles)
-constexpr int kBlk = 64;       // NS block edge for the transposed variants
+constexpr int kRows = 32;    // NS rows per gather/untile work item (plain tiles)
+constexpr int kVec = 8;      // 8-element vectors per thread per load batch
+constexpr int kBlk = 64;     // NS block edge for the transposed variants
 constexpr int kBlkPitch = kBlk + 8;
 
 struct Geo {
@@ -38,18 +44,101 @@ HM_DEV float momentum_elem(float g, float* m, float mu, bool nesterov, bool has_
 }
 
 // ---------------------------------------------------------------------------
-// Gather: work item = (tile, 64x64 block of the NS operand). The block's
-// parameter elements are read as 16-byte row segments, momentum is applied,
-// and bf16(e) is written twice: in the parameter's orientation straight from
-// registers, and transposed through LDS. For plain tiles (tile_h <= tile_w)
-// the parameter orientation is X (the NS operand) and the transpose is X^T;
-// for tall tiles the NS operand is the tile's transpose, so the roles swap.
-// X^T (tiles_t, (n_tiles, np, mp)) is optional.
+// Gather, plain tiles: work item = (tile t, slab q of kRows NS rows); NS row i
+// of tile (r, c) is parameter row r*tile_h + i, columns c*tile_w + j. Rows and
+// columns outside the tile or the parameter are written as zeros. The slab's
+// sum of squares of the bf16 values goes to partials[t * (mp / kRows) + q].
 // ---------------------------------------------------------------------------
-template <int DT, bool TRANS>
-__global__ __launch_bounds__(kThreads) void gather_kernel(
+template <int DT>
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(
     const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
-    uint16_t* __restrict__ tiles, uint16_t* __restrict__ tiles_t, float* __restrict__ partials) {
+    uint16_t* __restrict__ tiles, float* __restrict__ partials) {
+  __shared__ float red[kThreads / 64];
+  const int slabs = geo.mp / kRows;
+  const int vpr = geo.np / 8;          // 8-element vectors per NS row
+  const int per_item = kRows * vpr;
+  const int64_t total = n_tiles * slabs;
+  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+    const int64_t t = item / slabs;
+    const int q = (int)(item - t * slabs);
+    const HimuonParamDesc& P = params[find_param(params, n_params, t)];
+    const int64_t lt = t - P.tile0;
+    const int r = (int)(lt / P.C), c = (int)(lt % P.C);
+    const bool has_mom = P.momentum != nullptr;
+    const float mu = P.mu;
+    const bool nesterov = P.nesterov != 0;
+    uint16_t* out = tiles + t * (int64_t)geo.mp * geo.np;
+    float ssq = 0.f;
+    for (int v0 = 0; v0 < per_item; v0 += kThreads * kVec) {
+      float g[kVec][8], m[kVec][8];
+      bool fast[kVec];
+      // Phase 1: every load of the batch is issued before any is used.
+#pragma unroll
+      for (int k = 0; k < kVec; ++k) {
+        const int v = v0 + k * kThreads + threadIdx.x;
+        const int i = q * kRows + v / vpr, j0 = (v % vpr) * 8;
+        const int64_t pr = (int64_t)r * geo.tile_h + i, pc = (int64_t)c * geo.tile_w + j0;
+        const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
+        fast[k] = v < per_item && i < geo.tile_h && pr < P.h && j0 + 8 <= geo.tile_w && pc + 8 <= P.w &&
+                  aligned16<DT>(P.grad, og) && (!has_mom || aligned16<DT>(P.momentum, om));
+        if (fast[k]) {
+          load8<DT>(P.grad, og, g[k]);
+          if (has_mom) load8<DT>(P.momentum, om, m[k]);
+        }
+      }
+      // Phase 2: momentum, momentum store, bf16 NS operand store.
+#pragma unroll
+      for (int k = 0; k < kVec; ++k) {
+        const int v = v0 + k * kThreads + threadIdx.x;
+        if (v >= per_item) continue;
+        const int i = q * kRows + v / vpr, j0 = (v % vpr) * 8;
+        const int64_t pr = (int64_t)r * geo.tile_h + i, pc = (int64_t)c * geo.tile_w + j0;
+        const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
+        float x[8];
+        if (fast[k]) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = momentum_elem<DT>(g[k][e], &m[k][e], mu, nesterov, has_mom);
+          if (has_mom) store8<DT>(P.momentum, om, m[k]);
+        } else {
+          const bool row_ok = i < geo.tile_h && pr < P.h;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            x[e] = 0.f;
+            if (row_ok && j0 + e < geo.tile_w && pc + e < P.w) {
+              const float gv = load_elem<DT>(P.grad, og + e);
+              float mv = has_mom ? load_elem<DT>(P.momentum, om + e) : 0.f;
+              x[e] = momentum_elem<DT>(gv, &mv, mu, nesterov, has_mom);
+              if (has_mom) store_elem<DT>(P.momentum, om + e, mv);
+            }
+          }
+        }
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          h[e] = f32_to_bf16(x[e]);
+          const float f = bf16_to_f32(h[e]);
+          ssq = fmaf(f, f, ssq);
+        }
+        *reinterpret_cast<uint4*>(out + (int64_t)i * geo.np + j0) =
+            make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
+      }
+    }
+    const float sum = block_sum<kThreads>(ssq, red);
+    if (threadIdx.x == 0) partials[item] = sum;
+    __syncthreads();  // red[] is rewritten by the next item
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gather, tall tiles (tile_h > tile_w, the NS operand is the tile's
+// transpose): work item = (tile, 64x64 block of the NS operand). The block's
+// parameter elements are read as 16-byte row segments, momentum is applied,
+// and bf16(e) is transposed through LDS into the NS operand.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(kThreads) void gather_trans_kernel(
+    const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
+    uint16_t* __restrict__ tiles, float* __restrict__ partials) {
   __shared__ uint16_t sT[kBlk * kBlkPitch];  // [param col][param row] of the block
   __shared__ float red[kThreads / 64];
   const int bi_n = geo.mp / kBlk, bj_n = geo.np / kBlk;
@@ -59,19 +148,14 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
   const int64_t t = item / blocks;
   const int b = (int)(item % blocks);
   const int i0 = (b / bj_n) * kBlk, j0 = (b % bj_n) * kBlk;  // NS block origin
-  const int tr0 = TRANS ? j0 : i0, tc0 = TRANS ? i0 : j0;     // tile-local origin
+  const int tr0 = j0, tc0 = i0;                                // tile-local origin
   const HimuonParamDesc& P = params[find_param(params, n_params, t)];
   const int64_t lt = t - P.tile0;
   const int r = (int)(lt / P.C), c = (int)(lt % P.C);
   const bool has_mom = P.momentum != nullptr;
   const float mu = P.mu;
   const bool nesterov = P.nesterov != 0;
-  const int64_t tsz = (int64_t)geo.mp * geo.np;
-  // Destination in the parameter orientation: X rows (plain) or X^T rows (tall).
-  uint16_t* direct = TRANS ? (tiles_t ? tiles_t + t * tsz : nullptr) : tiles + t * tsz;
-  const int direct_ld = TRANS ? geo.mp : geo.np;
-  uint16_t* across = TRANS ? tiles + t * tsz : (tiles_t ? tiles_t + t * tsz : nullptr);
-  const int across_ld = TRANS ? geo.np : geo.mp;
+  uint16_t* ns = tiles + t * (int64_t)geo.mp * geo.np;
   float ssq = 0.f;
   for (int v = threadIdx.x; v < kBlk * (kBlk / 8); v += kThreads) {
     const int rr = v / (kBlk / 8), cv = v % (kBlk / 8);
@@ -102,25 +186,19 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
         }
       }
     }
-    uint32_t h[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      h[e] = f32_to_bf16(x[e]);
-      const float f = bf16_to_f32(h[e]);
+      const uint32_t h = f32_to_bf16(x[e]);
+      const float f = bf16_to_f32(h);
       ssq = fmaf(f, f, ssq);
-      if (across) sT[(cv * 8 + e) * kBlkPitch + rr] = (uint16_t)h[e];
+      sT[(cv * 8 + e) * kBlkPitch + rr] = (uint16_t)h;
     }
-    if (direct)
-      *reinterpret_cast<uint4*>(direct + (int64_t)(tr0 + rr) * direct_ld + tc) =
-          make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
   }
-  if (across) {
-    __syncthreads();
-    for (int v = threadIdx.x; v < kBlk * (kBlk / 8); v += kThreads) {
-      const int cc = v / (kBlk / 8), rv = v % (kBlk / 8);
-      const uint4 q = *reinterpret_cast<const uint4*>(&sT[cc * kBlkPitch + rv * 8]);
-      *reinterpret_cast<uint4*>(across + (int64_t)(tc0 + cc) * across_ld + tr0 + rv * 8) = q;
-    }
+  __syncthreads();
+  for (int v = threadIdx.x; v < kBlk * (kBlk / 8); v += kThreads) {
+    const int cc = v / (kBlk / 8), rv = v % (kBlk / 8);
+    const uint4 q = *reinterpret_cast<const uint4*>(&sT[cc * kBlkPitch + rv * 8]);
+    *reinterpret_cast<uint4*>(ns + (int64_t)(tc0 + cc) * geo.np + tr0 + rv * 8) = q;
   }
   const float s = block_sum<kThreads>(ssq, red);
   if (threadIdx.x == 0) partials[t * blocks + b] = s;
@@ -137,49 +215,60 @@ __global__ __launch_bounds__(kThreads) void tile_scale_kernel(const float* __res
 }
 
 // ---------------------------------------------------------------------------
-// Untile, plain tiles: update[pr, pc] = scale * NS(i, j).
+// Untile, plain tiles: update[pr, pc] = scale * NS(i, j). Work item = (tile,
+// slab of kRows NS rows); only NS columns < tile_w hold data.
 // ---------------------------------------------------------------------------
 template <int DT>
-__global__ __launch_bounds__(kThreads) void untile_plain_kernel(
+__global__ __launch_bounds__(kThreads) void untile_rows_kernel(
     const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
     const uint16_t* __restrict__ tiles) {
-  const int slabs = geo.mp / kSlabRows;
-  const int64_t item = xcd_item(n_tiles * slabs);
-  if (item >= n_tiles * slabs) return;
-  const int64_t t = item / slabs;
-  const int q = (int)(item % slabs);
-  const HimuonParamDesc& P = params[find_param(params, n_params, t)];
-  const int64_t lt = t - P.tile0;
-  const int r = (int)(lt / P.C), c = (int)(lt % P.C);
-  const float sc = P.upd_scale;
-  const int vpr = geo.np / 8;
-  const uint16_t* in = tiles + t * (int64_t)geo.mp * geo.np;
-  // Only NS columns < tile_w hold data.
+  const int slabs = geo.mp / kRows;
   const int vcols = (geo.tile_w + 7) / 8;
-  for (int v = threadIdx.x; v < kSlabRows * vcols; v += kThreads) {
-    const int i = q * kSlabRows + v / vcols;
-    const int j0 = (v % vcols) * 8;
-    const int64_t pr = (int64_t)r * geo.tile_h + i;
-    const int64_t pc = (int64_t)c * geo.tile_w + j0;
-    if (i >= geo.tile_h || pr >= P.h || pc >= P.w) continue;
-    const uint4 qv = *reinterpret_cast<const uint4*>(in + (int64_t)i * geo.np + j0);
-    const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
-    float y[8];
+  const int per_item = kRows * vcols;
+  const int64_t total = n_tiles * slabs;
+  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+    const int64_t t = item / slabs;
+    const int q = (int)(item - t * slabs);
+    const HimuonParamDesc& P = params[find_param(params, n_params, t)];
+    const int64_t lt = t - P.tile0;
+    const int r = (int)(lt / P.C), c = (int)(lt % P.C);
+    const float sc = P.upd_scale;
+    const uint16_t* in = tiles + t * (int64_t)geo.mp * geo.np;
+    for (int v0 = 0; v0 < per_item; v0 += kThreads * kVec) {
+      uint4 qv[kVec];
+      bool ok[kVec];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      y[2 * k] = sc * bf16_to_f32(w[k] & 0xffffu);
-      y[2 * k + 1] = sc * __uint_as_float(w[k] & 0xffff0000u);
-    }
-    const int64_t ou = pr * P.ld_upd + pc;
-    if (j0 + 8 <= geo.tile_w && pc + 8 <= P.w && aligned16<DT>(P.update, ou)) {
-      store8<DT>(P.update, ou, y);
-    } else {
+      for (int k = 0; k < kVec; ++k) {
+        const int v = v0 + k * kThreads + threadIdx.x;
+        const int i = q * kRows + v / vcols, j0 = (v % vcols) * 8;
+        const int64_t pr = (int64_t)r * geo.tile_h + i, pc = (int64_t)c * geo.tile_w + j0;
+        ok[k] = v < per_item && i < geo.tile_h && pr < P.h && pc < P.w;
+        if (ok[k]) qv[k] = *reinterpret_cast<const uint4*>(in + (int64_t)i * geo.np + j0);
+      }
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (j0 + e < geo.tile_w && pc + e < P.w) store_elem<DT>(P.update, ou + e, y[e]);
+      for (int k = 0; k < kVec; ++k) {
+        if (!ok[k]) continue;
+        const int v = v0 + k * kThreads + threadIdx.x;
+        const int i = q * kRows + v / vcols, j0 = (v % vcols) * 8;
+        const int64_t pr = (int64_t)r * geo.tile_h + i, pc = (int64_t)c * geo.tile_w + j0;
+        const uint32_t w[4] = {qv[k].x, qv[k].y, qv[k].z, qv[k].w};
+        float y[8];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          y[2 * e2] = sc * bf16_to_f32(w[e2] & 0xffffu);
+          y[2 * e2 + 1] = sc * __uint_as_float(w[e2] & 0xffff0000u);
+        }
+        const int64_t ou = pr * P.ld_upd + pc;
+        if (j0 + 8 <= geo.tile_w && pc + 8 <= P.w && aligned16<DT>(P.update, ou)) {
+          store8<DT>(P.update, ou, y);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (j0 + e < geo.tile_w && pc + e < P.w) store_elem<DT>(P.update, ou + e, y[e]);
+        }
+      }
     }
   }
-  (void)vpr;
 }
 
 // Untile, transposed tiles: update[pr, pc] = scale * NS(pc_local, pr_local).
@@ -238,6 +327,14 @@ __global__ __launch_bounds__(kThreads) void untile_trans_kernel(
   }
 }
 
+int num_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  return n;
+}
+
 bool geo_ok(int tile_h, int tile_w, int mp, int np) {
   const int m = tile_h <= tile_w ? tile_h : tile_w;
   const int n = tile_h <= tile_w ? tile_w : tile_h;
@@ -252,36 +349,38 @@ bool geo_ok(int tile_h, int tile_w, int mp, int np) {
 // ---------------------------------------------------------------------------
 extern "C" int himuon_gather_partials_per_tile(int tile_h, int tile_w, int mp, int np) {
   if (!geo_ok(tile_h, tile_w, mp, np)) return HIMUON_EINVAL;
-  return (mp / kBlk) * (np / kBlk);
+  return tile_h > tile_w ? (mp / kBlk) * (np / kBlk) : mp / kRows;
 }
 
 extern "C" int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_params,
                                       int64_t n_tiles, int tile_h, int tile_w, int mp, int np,
-                                      int dtype, uint16_t* tiles_bf16, uint16_t* tiles_t_bf16,
-                                      float* partials, void* stream) {
+                                      int dtype, uint16_t* tiles_bf16, float* partials,
+                                      void* stream) {
   if (!geo_ok(tile_h, tile_w, mp, np) || n_params <= 0 || n_tiles < 0 || !params_dev ||
       !tiles_bf16 || !partials)
     return HIMUON_EINVAL;
   if (n_tiles == 0) return 0;
   const Geo geo{tile_h, tile_w, mp, np};
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool trans = tile_h > tile_w;
   const int64_t items = n_tiles * himuon_gather_partials_per_tile(tile_h, tile_w, mp, np);
-  const dim3 grid((unsigned)xcd_grid(items)), block(kThreads);
-#define HM_GATHER(DT)                                                                       \
-  if (trans)                                                                                \
-    hipLaunchKernelGGL((gather_kernel<DT, true>), grid, block, 0, s, params_dev, n_params,   \
-                       n_tiles, geo, tiles_bf16, tiles_t_bf16, partials);                   \
-  else                                                                                      \
-    hipLaunchKernelGGL((gather_kernel<DT, false>), grid, block, 0, s, params_dev, n_params,  \
-                       n_tiles, geo, tiles_bf16, tiles_t_bf16, partials);
-  switch (dtype) {
-    case HIMUON_DTYPE_F32: HM_GATHER(HIMUON_DTYPE_F32); break;
-    case HIMUON_DTYPE_BF16: HM_GATHER(HIMUON_DTYPE_BF16); break;
-    case HIMUON_DTYPE_F16: HM_GATHER(HIMUON_DTYPE_F16); break;
-    default: return HIMUON_EINVAL;
+  const dim3 block(kThreads);
+  if (tile_h > tile_w) {
+    const dim3 grid((unsigned)xcd_grid(items));
+    switch (dtype) {
+      case HIMUON_DTYPE_F32: hipLaunchKernelGGL(gather_trans_kernel<HIMUON_DTYPE_F32>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, partials); break;
+      case HIMUON_DTYPE_BF16: hipLaunchKernelGGL(gather_trans_kernel<HIMUON_DTYPE_BF16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, partials); break;
+      case HIMUON_DTYPE_F16: hipLaunchKernelGGL(gather_trans_kernel<HIMUON_DTYPE_F16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, partials); break;
+      default: return HIMUON_EINVAL;
+    }
+  } else {
+    const dim3 grid((unsigned)std::min<int64_t>(items, (int64_t)4 * num_cus()));
+    switch (dtype) {
+      case HIMUON_DTYPE_F32: hipLaunchKernelGGL(gather_rows_kernel<HIMUON_DTYPE_F32>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, partials); break;
+      case HIMUON_DTYPE_BF16: hipLaunchKernelGGL(gather_rows_kernel<HIMUON_DTYPE_BF16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, partials); break;
+      case HIMUON_DTYPE_F16: hipLaunchKernelGGL(gather_rows_kernel<HIMUON_DTYPE_F16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, partials); break;
+      default: return HIMUON_EINVAL;
+    }
   }
-#undef HM_GATHER
   return (int)hipGetLastError();
 }
 
@@ -304,22 +403,23 @@ extern "C" int himuon_untile(const HimuonParamDesc* params_dev, int n_params, in
   if (n_tiles == 0) return 0;
   const Geo geo{tile_h, tile_w, mp, np};
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool trans = tile_h > tile_w;
-  const int64_t items = n_tiles * (trans ? (mp / kBlk) * (np / kBlk) : mp / kSlabRows);
-  const dim3 grid((unsigned)xcd_grid(items)), block(kThreads);
-#define HM_UNTILE(DT)                                                                           \
-  if (trans)                                                                                    \
-    hipLaunchKernelGGL(untile_trans_kernel<DT>, grid, block, 0, s, params_dev, n_params, n_tiles, \
-                       geo, tiles_bf16);                                                         \
-  else                                                                                          \
-    hipLaunchKernelGGL(untile_plain_kernel<DT>, grid, block, 0, s, params_dev, n_params, n_tiles, \
-                       geo, tiles_bf16);
-  switch (dtype) {
-    case HIMUON_DTYPE_F32: HM_UNTILE(HIMUON_DTYPE_F32); break;
-    case HIMUON_DTYPE_BF16: HM_UNTILE(HIMUON_DTYPE_BF16); break;
-    case HIMUON_DTYPE_F16: HM_UNTILE(HIMUON_DTYPE_F16); break;
-    default: return HIMUON_EINVAL;
+  const dim3 block(kThreads);
+  if (tile_h > tile_w) {
+    const dim3 grid((unsigned)xcd_grid(n_tiles * (mp / kBlk) * (np / kBlk)));
+    switch (dtype) {
+      case HIMUON_DTYPE_F32: hipLaunchKernelGGL(untile_trans_kernel<HIMUON_DTYPE_F32>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
+      case HIMUON_DTYPE_BF16: hipLaunchKernelGGL(untile_trans_kernel<HIMUON_DTYPE_BF16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
+      case HIMUON_DTYPE_F16: hipLaunchKernelGGL(untile_trans_kernel<HIMUON_DTYPE_F16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
+      default: return HIMUON_EINVAL;
+    }
+  } else {
+    const dim3 grid((unsigned)std::min<int64_t>(n_tiles * (mp / kRows), (int64_t)4 * num_cus()));
+    switch (dtype) {
+      case HIMUON_DTYPE_F32: hipLaunchKernelGGL(untile_rows_kernel<HIMUON_DTYPE_F32>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
+      case HIMUON_DTYPE_BF16: hipLaunchKernelGGL(untile_rows_kernel<HIMUON_DTYPE_BF16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
+      case HIMUON_DTYPE_F16: hipLaunchKernelGGL(untile_rows_kernel<HIMUON_DTYPE_F16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
+      default: return HIMUON_EINVAL;
+    }
   }
-#undef HM_UNTILE
   return (int)hipGetLastError();
 }

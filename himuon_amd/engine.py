@@ -5,7 +5,7 @@ device, allocated once so pointers stay stable for hipGraph capture:
 
 * the bf16 NS tile buffers ``(n_tiles, mp, np)`` (the concat buffer of
   himuon.py:588-612, stored directly as the bf16 NS operand) that X
-  ping-pongs between, plus their transposes when the NT kernel runs,
+  ping-pongs between,
 * the per-tile sum-of-squares partials and normalisers,
 * the per-parameter ``update`` tensors (grad dtype) the untile kernel writes,
 * the device descriptor table (HimuonParamDesc[]) the gather/untile kernels read.
@@ -47,14 +47,10 @@ class TileGroup:
         self.tile0 = [sum(counts[:i]) for i in range(len(counts))]
         self.n_tiles = sum(counts)
         self.ppt = nat.gather_partials_per_tile(self.tile_h, self.tile_w, self.mp, self.np)
-        shape, shape_t = (self.n_tiles, self.mp, self.np), (self.n_tiles, self.np, self.mp)
-        # X ping-pongs between tiles and alt through the NS iterations; the
-        # transposed copies exist only for the persistent NT kernel.
+        shape = (self.n_tiles, self.mp, self.np)
+        # X ping-pongs between tiles and alt through the NS iterations.
         self.tiles = torch.empty(shape, device=device, dtype=torch.bfloat16)
         self.alt = torch.empty(shape, device=device, dtype=torch.bfloat16)
-        nt = nat.nt_path(self.mp, self.np)
-        self.tiles_t = torch.empty(shape_t, device=device, dtype=torch.bfloat16) if nt else None
-        self.alt_t = torch.empty(shape_t, device=device, dtype=torch.bfloat16) if nt else None
         self.partials = torch.empty((self.n_tiles, self.ppt), device=device, dtype=torch.float32)
         self.inv = torch.empty((self.n_tiles,), device=device, dtype=torch.float32)
         self.updates = [torch.empty(g.shape, device=device, dtype=dtype) for g in grads]
@@ -112,7 +108,7 @@ class TileGroup:
     def gather(self) -> None:
         nat.momentum_gather(
             self.desc, len(self.updates), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
-            self.dtype, self.tiles, self.tiles_t, self.partials,
+            self.dtype, self.tiles, self.partials,
         )
         nat.tile_scale(self.partials, self.ppt, self.n_tiles, self.inv)
 
@@ -125,8 +121,8 @@ class TileGroup:
             return
         r = self._rng
         nat.ns5(
-            r(self.tiles, start, count), r(self.tiles_t, start, count), r(self.alt, start, count),
-            r(self.alt_t, start, count), self.inv[start : start + count], count, self.mp, self.np, steps,
+            r(self.tiles, start, count), r(self.alt, start, count),
+            self.inv[start : start + count], count, self.mp, self.np, steps,
             workspace, sub_batch,
         )
 

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HIMUON_ABI_VERSION 1
+#define HIMUON_ABI_VERSION 2
 
 /* Element type codes for gradients / momentum / updates. */
 #define HIMUON_DTYPE_F32 0
@@ -97,17 +97,16 @@ int himuon_gather_partials_per_tile(int tile_h, int tile_w, int mp, int np);
  * and sum separately, e is one fused multiply-add, as torch's in-place mul_,
  * add_ and add(alpha=) evaluate them). If momentum is NULL, e = g and
  * nothing is written back. bf16(e) is stored at its NS tile position in
- * tiles_bf16 (n_tiles, mp, np) and, if tiles_t_bf16 is not NULL, at the
- * transposed position in tiles_t_bf16 (n_tiles, np, mp); padding is written
- * as zero. partials[t * P + q] receives the fp32 sum of squares of the bf16
- * values of the q-th 64x64 block of NS tile t, P =
- * himuon_gather_partials_per_tile(...).
+ * tiles_bf16 (n_tiles, mp, np); padding is written as zero. partials[t * P +
+ * q] receives the fp32 sum of squares of the bf16 values of the q-th part of
+ * NS tile t, P = himuon_gather_partials_per_tile(...): slabs of 32 NS rows
+ * (P = mp / 32) when tile_h <= tile_w, 64x64 blocks (P = mp/64 * np/64) for
+ * tall tiles.
  */
 int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_params,
                            int64_t n_tiles, int tile_h, int tile_w, int mp,
                            int np, int dtype, uint16_t* tiles_bf16,
-                           uint16_t* tiles_t_bf16, float* partials,
-                           void* stream);
+                           float* partials, void* stream);
 
 /*
  * Per-tile normaliser: inv[t] = 1 / (sqrt(sum_q partials[t*P+q]) + eps).
@@ -118,7 +117,8 @@ int himuon_tile_scale(const float* partials, int partials_per_tile,
                       int64_t n_tiles, float eps, float* inv, void* stream);
 
 /* Workspace bytes himuon_ns5 needs for a given sub-batch size (the A and B
- * intermediates of `sub_batch` tiles). */
+ * intermediates of `sub_batch` tiles, then the counters of the dataflow
+ * kernel variant). */
 size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np);
 
 /*
@@ -135,16 +135,15 @@ size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np);
  *
  * x, y: (n_tiles, mp, np) bf16; X ping-pongs between them, so the result is
  * in x when `steps` is even and in y when it is odd (x is overwritten).
- * xt, yt: optional (n_tiles, np, mp) transposed copies (both or neither);
- * xt must hold X0^T as written by himuon_momentum_gather. With them, tiles
- * whose mp and np are multiples of 256 run on the persistent 256-block path.
- * Tiles are processed in sub-batches of `sub_batch`; the workspace must hold
+ * Tiles whose mp and np are multiples of 256 run on persistent 256x256-block
+ * kernels, others on 128x128-block kernels. Tiles are processed in
+ * sub-batches of `sub_batch`; the workspace must hold
  * himuon_ns5_workspace_bytes(sub_batch, mp, np) bytes.
  */
-int himuon_ns5(uint16_t* x, uint16_t* xt, uint16_t* y, uint16_t* yt,
-               const float* inv, int64_t n_tiles, int mp, int np, int steps,
-               float a, float b, float c, void* workspace,
-               size_t workspace_bytes, int64_t sub_batch, void* stream);
+int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles,
+               int mp, int np, int steps, float a, float b, float c,
+               void* workspace, size_t workspace_bytes, int64_t sub_batch,
+               void* stream);
 
 /*
  * Untile/scatter: for every element of every parameter,

@@ -57,35 +57,30 @@ def test_desc_layout_matches_header():
 
 
 def test_partials_per_tile(lib):
-    assert lib.himuon_gather_partials_per_tile(512, 512, 512, 512) == (512 // 64) ** 2
-    assert lib.himuon_gather_partials_per_tile(1024, 512, 512, 1024) == (512 // 64) * (1024 // 64)
+    assert lib.himuon_gather_partials_per_tile(512, 512, 512, 512) == 512 // 32  # 32-row slabs
+    assert lib.himuon_gather_partials_per_tile(256, 1024, 256, 1024) == 256 // 32
+    assert lib.himuon_gather_partials_per_tile(1024, 512, 512, 1024) == (512 // 64) * (1024 // 64)  # tall: 64x64 blocks
     assert lib.himuon_gather_partials_per_tile(512, 512, 500, 512) == -22  # not aligned
     assert lib.himuon_gather_partials_per_tile(512, 512, 384, 512) == -22  # mp < m
 
 
 def test_workspace_bytes(lib):
-    # A and B per sub-batch tile (256-byte aligned), then the dataflow counters:
-    # prog[n], 32 ints of queue state, wseq[16][n + 1].
-    n = 4
-    ab = 2 * n * 512 * 512 * 2
-    assert lib.himuon_ns5_workspace_bytes(n, 512, 512) == ab + 4 * (n + 32 + 16 * (n + 1))
-    assert lib.himuon_ns5_workspace_bytes(3, 128, 256) == ((2 * 3 * 128 * 128 * 2 + 255) // 256) * 256 + 4 * (3 + 32 + 16 * 4)
+    assert lib.himuon_ns5_workspace_bytes(4, 512, 512) == 2 * 4 * 512 * 512 * 2  # A and B
     assert lib.himuon_ns5_workspace_bytes(0, 512, 512) == 0
 
 
 def test_argument_errors_return_before_launch(lib):
     z = None
     # null descriptor / buffers
-    assert lib.himuon_momentum_gather(z, 1, 4, 512, 512, 512, 512, 0, z, z, z, z) == -22
+    assert lib.himuon_momentum_gather(z, 1, 4, 512, 512, 512, 512, 0, z, z, z) == -22
     # bad dtype code with otherwise valid (dummy) pointers: still rejected on the host
-    assert lib.himuon_momentum_gather(8, 1, 4, 512, 512, 512, 512, 9, 8, z, 8, z) == -22
+    assert lib.himuon_momentum_gather(8, 1, 4, 512, 512, 512, 512, 9, 8, 8, z) == -22
     # mp > np is not an NS geometry
-    assert lib.himuon_ns5(8, z, 16, z, 8, 4, 1024, 512, 5, 1.0, 1.0, 1.0, 8, 1 << 30, 4, z) == -22
-    # x and y must be distinct; xt and yt both or neither
-    assert lib.himuon_ns5(8, z, 8, z, 8, 4, 512, 512, 5, 1.0, 1.0, 1.0, 8, 1 << 30, 4, z) == -22
-    assert lib.himuon_ns5(8, 16, 24, z, 8, 4, 512, 512, 5, 1.0, 1.0, 1.0, 8, 1 << 30, 4, z) == -22
+    assert lib.himuon_ns5(8, 16, 8, 4, 1024, 512, 5, 1.0, 1.0, 1.0, 8, 1 << 30, 4, z) == -22
+    # x and y must be distinct
+    assert lib.himuon_ns5(8, 8, 8, 4, 512, 512, 5, 1.0, 1.0, 1.0, 8, 1 << 30, 4, z) == -22
     # workspace too small
-    assert lib.himuon_ns5(8, z, 16, z, 8, 4, 512, 512, 5, 1.0, 1.0, 1.0, 8, 16, 4, z) == -28
+    assert lib.himuon_ns5(8, 16, 8, 4, 512, 512, 5, 1.0, 1.0, 1.0, 8, 16, 4, z) == -28
     assert lib.himuon_untile(z, 1, 4, 512, 512, 512, 512, 0, z, z) == -22
     assert lib.himuon_tile_scale(z, 16, 4, 1e-7, z, z) == -22
     # empty work is a no-op success
