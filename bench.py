@@ -47,6 +47,11 @@ def ns_path() -> str:
 
 PEAK_HBM_GBS = 8000.0
 
+# HBM bytes the NS5 stage moves per step, from rocprofv3 --pmc FETCH_SIZE /
+# WRITE_SIZE (scaled by a 256 MiB copy of known size) on this config; see
+# profiles/himuon_step_qwen3-4b_t512.md. Other configs: not measured (null).
+NS5_STAGE_TRAFFIC_BYTES = {"qwen3-4b": 321.69e9}
+
 CONFIGS = {
     # name: (layers, [(h, w) per layer], tile_size, param dtype, description)
     "qwen3-4b": (36, [(4096, 2560), (1024, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (9728, 2560), (2560, 9728)],
@@ -131,6 +136,22 @@ def time_io_stage(opt, reps: int) -> tuple[float, float]:
     return ev[0].elapsed_time(ev[1]) / reps, ev[1].elapsed_time(ev[2]) / reps
 
 
+def time_apply(opt, reps: int) -> float:
+    """Average ms of the outside-graph WD + LR application of one step (the
+    multi-tensor HIP launch), HIP events on the current stream."""
+    s = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    opt._apply_pending_updates()
+    torch.cuda.synchronize()
+    e0.record(s)
+    for _ in range(reps):
+        opt._apply_pending_updates()
+    e1.record(s)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
 def cpu_baseline(layers, shapes, tile, budget_s: float = 20.0):
     """The CPU oracle (numpy, bf16-staged NS5) on a bounded sample of the same
     workload: the matrices of one layer (or as many of its tiles as fit the time
@@ -211,6 +232,12 @@ def main():
     from himuon_amd.optimizers.himuon import HiMuon
 
     load()
+    # A 256 MiB device copy of known size: under `rocprofv3 --pmc` its
+    # FETCH_SIZE / WRITE_SIZE readings calibrate those counters (a plain copy
+    # reads and writes exactly 256 MiB), so kernel traffic can be scaled.
+    cal = torch.empty(64 << 20, device="cuda", dtype=torch.float32)
+    torch.empty_like(cal).copy_(cal)
+    del cal
     layers, shapes, tile, pdtype, desc = CONFIGS[args.config]
     params = build_params(layers, shapes, pdtype)
     opt = HiMuon([{"params": params, "use_muon": True}], lr=1e-2, weight_decay=0.1, tile_size=tile,
@@ -235,8 +262,10 @@ def main():
 
     ns_ms = time_ns_stage(opt, reps=max(3, args.steps // 2))
     gather_ms, untile_ms = time_io_stage(opt, reps=max(3, args.steps // 2))
+    apply_ms = time_apply(opt, reps=max(3, args.steps // 2))
     flops = algorithmic_flops(opt)
     n_tiles = sum(g["tiles"].n_tiles for g in opt._groups)
+    traffic = NS5_STAGE_TRAFFIC_BYTES.get(args.config) if ns_path() == "stream" else None
     n_el = sum(p.numel() for p in params)
     ns_tflops = flops / (ns_ms * 1e-3) / 1e12
 
@@ -271,6 +300,8 @@ def main():
         "gather_gbs": round(14.0 * n_el / (gather_ms * 1e-3) / 1e9, 1),
         "untile_ms": round(untile_ms, 3),
         "untile_gbs": round(6.0 * n_el / (untile_ms * 1e-3) / 1e9, 1),
+        "apply_ms": round(apply_ms, 3),
+        "apply_gbs": round(8.0 * n_el / (apply_ms * 1e-3) / 1e9, 1) if pdtype == torch.bfloat16 else None,
         "roofline": {
             "kernel": NS_KERNELS.get(ns_path(), ns_path()),
             "bound": "mfma",
@@ -278,7 +309,9 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(ns_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_gbs": round(traffic / (ns_ms * 1e-3) / 1e9, 1) if traffic else None,
+            "traffic_frac_hbm_peak": round(traffic / (ns_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if traffic else None,
         },
     }
     if not args.no_cpu_baseline:
