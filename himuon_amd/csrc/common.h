@@ -9,6 +9,7 @@
 #include "../../include/himuon_hip.h"
 
 #define HM_DEV __device__ __forceinline__
+#define HM_HD __host__ __device__ __forceinline__
 
 // ---------------------------------------------------------------------------
 // bf16 / fp16 <-> fp32. Rounding is round-to-nearest-even with quiet NaNs,

@@ -313,11 +313,14 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_
   uint16_t* wsA = static_cast<uint16_t*>(workspace);
   uint16_t* wsB = wsA + sb * sq;
   // Tiles whose padded edges are multiples of 256 run the persistent
-  // streamed-operand kernels (ns5_stream.hip); HIMUON_NS_PATH=small selects the
-  // 128-block kernels below for them too (comparison runs). Other tiles always
-  // run the 128-block kernels.
+  // streamed-operand kernels (ns5_stream.hip); tiles with mp == 128 and
+  // np <= 256 run the fused LDS-resident kernel (ns5_lds.hip);
+  // HIMUON_NS_PATH=small selects the 128-block kernels below for both
+  // (comparison runs). Other tiles always run the 128-block kernels.
   const char* path = getenv("HIMUON_NS_PATH");
-  const bool st = ns5_stream_supported(mp, np) && !(path && path[0] == 's' && path[1] == 'm');
+  const bool small = path && path[0] == 's' && path[1] == 'm';
+  const bool st = ns5_stream_supported(mp, np) && !small;
+  const bool lds = ns5_lds_supported(mp, np) && !small;
   const int nb = mp / BM;
   const int npairs = nb * (nb + 1) / 2;
   const int apply_blocks = (mp / BM) * (np / BN);
@@ -325,7 +328,9 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_
   for (int64_t s0 = 0; s0 < n_tiles; s0 += sb) {
     const int64_t cnt = std::min<int64_t>(sb, n_tiles - s0);
     const int64_t o = s0 * rect;
-    if (st) {
+    if (lds) {
+      ns5_lds_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, s);
+    } else if (st) {
       ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
     } else {
       const uint16_t* cur = x + o;

@@ -27,9 +27,90 @@ HM_DEV u32x4_t scale8(u32x4_t v, float s) {
 
 HM_DEV uint32_t half16(uint32_t w, int h) { return h ? (w >> 16) : (w & 0xffffu); }
 
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __attribute__((address_space(3))) const u32x4_t lds_cu32x4;
+typedef __attribute__((address_space(3))) const u32x2_t lds_cu32x2;
+typedef __attribute__((address_space(3))) u32x2_t lds_u32x2;
+
+// v_mfma_f32_32x32x16_bf16: 8 bf16 of A (row l%32) and of B (column l%32) per lane,
+// k = 8 (l/32) .. + 7; the 32x32 fp32 result has row 8 (r/4) + 4 (l/32) + r%4,
+// column l%32 in register r of lane l.
+HM_DEV f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// bf16 pair (RNE, hardware v_cvt_pk_bf16_f32): lo in bits 0..15.
+HM_DEV uint32_t pk_bf16(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t r;
+  r[0] = (__bf16)lo;
+  r[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// s_waitcnt with vmcnt = N (expcnt and lgkmcnt at their maxima) / lgkmcnt = N.
+template <int N>
+HM_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+template <int N>
+HM_DEV void wait_lgkm() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));
+}
+
+// ds_read_b64_tr_b16 at an LDS byte address. Issued as inline assembly: the
+// compiler cannot tell these reads apart from the direct-to-LDS loads in
+// flight and would put a vmcnt(0) wait (draining the operand stream) before
+// the builtin. The result is only valid after an explicit lgkmcnt wait.
+HM_DEV u32x2_t ds_read_tr16(uint32_t addr) {
+  u32x2_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+// DPP quad permutations.
+HM_DEV uint32_t quad_swap2(uint32_t v) {  // lane ^ 2
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+}
+HM_DEV uint32_t quad_swap1(uint32_t v) {  // lane ^ 1
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+}
+
+// 4x4 bf16 transpose across a lane quad: lane k holds row k as (w0, w1) =
+// columns (0,1), (2,3); returns column k as rows (0,1), (2,3).
+HM_DEV u32x2_t quad_transpose(u32x2_t w, int k) {
+  const uint32_t send_a = (k < 2) ? w[1] : w[0];
+  const uint32_t recv_a = quad_swap2(send_a);
+  const uint32_t x = (k < 2) ? w[0] : recv_a;
+  const uint32_t y = (k < 2) ? recv_a : w[1];
+  const bool odd = k & 1;
+  const uint32_t send_b = odd ? ((x & 0xffffu) | (y << 16)) : ((x >> 16) | (y & 0xffff0000u));
+  const uint32_t r = quad_swap1(send_b);
+  u32x2_t o;
+  if (odd) {
+    o[0] = (r & 0xffffu) | (x & 0xffff0000u);
+    o[1] = (r >> 16) | (y & 0xffff0000u);
+  } else {
+    o[0] = (x & 0xffffu) | (r << 16);
+    o[1] = (y & 0xffffu) | (r & 0xffff0000u);
+  }
+  return o;
+}
+
+
 // Persistent streamed-operand 256-block path (ns5_stream.hip): mp, np
 // multiples of 256. Scales x in place (X0), then runs `steps` iterations on
 // `cnt` tiles, ping-ponging X between x and y.
 bool ns5_stream_supported(int mp, int np);
 void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
                     float a, float b, float c, uint16_t* wsA, uint16_t* wsB, hipStream_t s);
+
+// Fused LDS-resident path (ns5_lds.hip): mp == 128, np = 128 or 256. Runs
+// `steps` >= 1 iterations of `cnt` tiles in one launch; reads X from x and
+// leaves the result in x (even `steps`) or y (odd), as the other paths do.
+bool ns5_lds_supported(int mp, int np);
+void ns5_lds_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
+                 float a, float b, float c, hipStream_t s);

@@ -7,7 +7,8 @@
 // All are HBM-bound: each element is read/written once (14 B/el for fp32
 // gather, 6 B/el for fp32 untile), with 16-byte accesses on both sides.
 // Plain tiles (tile_h <= tile_w) move whole NS rows: a work item is a slab of
-// kRows rows of one tile, walked by a persistent grid, and each thread issues
+// 16384 / np rows of one tile (whole tiles up to 128 x 128), walked by a
+// persistent grid, and each thread issues
 // the loads of kVec 8-element vectors before using any of them, so enough
 // bytes are in flight to cover the memory latency. Tall tiles are transposed
 // through LDS in 64 x 64 blocks.
@@ -16,7 +17,7 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRows = 32;    // NS rows per gather/untile work item (plain tiles)
+constexpr int kSlabElems = 16384;  // NS elements per gather/untile work item (plain tiles)
 constexpr int kVec = 8;      // 8-element vectors per thread per load batch
 constexpr int kBlk = 64;     // NS block edge for the transposed variants
 constexpr int kBlkPitch = kBlk + 8;
@@ -24,6 +25,14 @@ constexpr int kBlkPitch = kBlk + 8;
 struct Geo {
   int tile_h, tile_w, mp, np;
 };
+
+// NS rows per plain-tile work item: kSlabElems / np (whole tiles at np = 128),
+// at least 32 and at most mp; mp and np are multiples of 128, so it divides mp.
+HM_HD int slab_rows(int mp, int np) {
+  int r = kSlabElems / np;
+  r = r < 32 ? 32 : r;
+  return r > mp ? mp : r;
+}
 
 // Momentum for one element (himuon.py:354-356); returns the NS input and
 // writes the new momentum value to *m. Results are rounded to the tensor
@@ -44,19 +53,21 @@ HM_DEV float momentum_elem(float g, float* m, float mu, bool nesterov, bool has_
 }
 
 // ---------------------------------------------------------------------------
-// Gather, plain tiles: work item = (tile t, slab q of kRows NS rows); NS row i
+// Gather, plain tiles: work item = (tile t, slab q of `rows` NS rows, rows =
+// slab_rows(mp, np)); NS row i
 // of tile (r, c) is parameter row r*tile_h + i, columns c*tile_w + j. Rows and
 // columns outside the tile or the parameter are written as zeros. The slab's
-// sum of squares of the bf16 values goes to partials[t * (mp / kRows) + q].
+// sum of squares of the bf16 values goes to partials[t * (mp / rows) + q].
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
     const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
     uint16_t* __restrict__ tiles, float* __restrict__ partials) {
   __shared__ float red[kThreads / 64];
-  const int slabs = geo.mp / kRows;
+  const int rows = slab_rows(geo.mp, geo.np);
+  const int slabs = geo.mp / rows;
   const int vpr = geo.np / 8;          // 8-element vectors per NS row
-  const int per_item = kRows * vpr;
+  const int per_item = rows * vpr;
   const int64_t total = n_tiles * slabs;
   for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
     const int64_t t = item / slabs;
@@ -76,7 +87,7 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
 #pragma unroll
       for (int k = 0; k < kVec; ++k) {
         const int v = v0 + k * kThreads + threadIdx.x;
-        const int i = q * kRows + v / vpr, j0 = (v % vpr) * 8;
+        const int i = q * rows + v / vpr, j0 = (v % vpr) * 8;
         const int64_t pr = (int64_t)r * geo.tile_h + i, pc = (int64_t)c * geo.tile_w + j0;
         const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
         fast[k] = v < per_item && i < geo.tile_h && pr < P.h && j0 + 8 <= geo.tile_w && pc + 8 <= P.w &&
@@ -91,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
       for (int k = 0; k < kVec; ++k) {
         const int v = v0 + k * kThreads + threadIdx.x;
         if (v >= per_item) continue;
-        const int i = q * kRows + v / vpr, j0 = (v % vpr) * 8;
+        const int i = q * rows + v / vpr, j0 = (v % vpr) * 8;
         const int64_t pr = (int64_t)r * geo.tile_h + i, pc = (int64_t)c * geo.tile_w + j0;
         const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
         float x[8];
@@ -216,15 +227,16 @@ __global__ __launch_bounds__(kThreads) void tile_scale_kernel(const float* __res
 
 // ---------------------------------------------------------------------------
 // Untile, plain tiles: update[pr, pc] = scale * NS(i, j). Work item = (tile,
-// slab of kRows NS rows); only NS columns < tile_w hold data.
+// slab of `rows` NS rows); only NS columns < tile_w hold data.
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(kThreads) void untile_rows_kernel(
     const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
     const uint16_t* __restrict__ tiles) {
-  const int slabs = geo.mp / kRows;
+  const int rows = slab_rows(geo.mp, geo.np);
+  const int slabs = geo.mp / rows;
   const int vcols = (geo.tile_w + 7) / 8;
-  const int per_item = kRows * vcols;
+  const int per_item = rows * vcols;
   const int64_t total = n_tiles * slabs;
   for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
     const int64_t t = item / slabs;
@@ -240,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void untile_rows_kernel(
 #pragma unroll
       for (int k = 0; k < kVec; ++k) {
         const int v = v0 + k * kThreads + threadIdx.x;
-        const int i = q * kRows + v / vcols, j0 = (v % vcols) * 8;
+        const int i = q * rows + v / vcols, j0 = (v % vcols) * 8;
         const int64_t pr = (int64_t)r * geo.tile_h + i, pc = (int64_t)c * geo.tile_w + j0;
         ok[k] = v < per_item && i < geo.tile_h && pr < P.h && pc < P.w;
         if (ok[k]) qv[k] = *reinterpret_cast<const uint4*>(in + (int64_t)i * geo.np + j0);
@@ -249,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void untile_rows_kernel(
       for (int k = 0; k < kVec; ++k) {
         if (!ok[k]) continue;
         const int v = v0 + k * kThreads + threadIdx.x;
-        const int i = q * kRows + v / vcols, j0 = (v % vcols) * 8;
+        const int i = q * rows + v / vcols, j0 = (v % vcols) * 8;
         const int64_t pr = (int64_t)r * geo.tile_h + i, pc = (int64_t)c * geo.tile_w + j0;
         const uint32_t w[4] = {qv[k].x, qv[k].y, qv[k].z, qv[k].w};
         float y[8];
@@ -349,7 +361,7 @@ bool geo_ok(int tile_h, int tile_w, int mp, int np) {
 // ---------------------------------------------------------------------------
 extern "C" int himuon_gather_partials_per_tile(int tile_h, int tile_w, int mp, int np) {
   if (!geo_ok(tile_h, tile_w, mp, np)) return HIMUON_EINVAL;
-  return tile_h > tile_w ? (mp / kBlk) * (np / kBlk) : mp / kRows;
+  return tile_h > tile_w ? (mp / kBlk) * (np / kBlk) : mp / slab_rows(mp, np);
 }
 
 extern "C" int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_params,
@@ -413,7 +425,7 @@ extern "C" int himuon_untile(const HimuonParamDesc* params_dev, int n_params, in
       default: return HIMUON_EINVAL;
     }
   } else {
-    const dim3 grid((unsigned)std::min<int64_t>(n_tiles * (mp / kRows), (int64_t)4 * num_cus()));
+    const dim3 grid((unsigned)std::min<int64_t>(n_tiles * (mp / slab_rows(mp, np)), (int64_t)4 * num_cus()));
     switch (dtype) {
       case HIMUON_DTYPE_F32: hipLaunchKernelGGL(untile_rows_kernel<HIMUON_DTYPE_F32>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
       case HIMUON_DTYPE_BF16: hipLaunchKernelGGL(untile_rows_kernel<HIMUON_DTYPE_BF16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;

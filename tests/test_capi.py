@@ -59,6 +59,8 @@ def test_desc_layout_matches_header():
 def test_partials_per_tile(lib):
     assert lib.himuon_gather_partials_per_tile(512, 512, 512, 512) == 512 // 32  # 32-row slabs
     assert lib.himuon_gather_partials_per_tile(256, 1024, 256, 1024) == 256 // 32
+    assert lib.himuon_gather_partials_per_tile(128, 128, 128, 128) == 1  # whole 128x128 tiles
+    assert lib.himuon_gather_partials_per_tile(256, 256, 256, 256) == 4  # 64-row slabs
     assert lib.himuon_gather_partials_per_tile(1024, 512, 512, 1024) == (512 // 64) * (1024 // 64)  # tall: 64x64 blocks
     assert lib.himuon_gather_partials_per_tile(512, 512, 500, 512) == -22  # not aligned
     assert lib.himuon_gather_partials_per_tile(512, 512, 384, 512) == -22  # mp < m
