@@ -12,7 +12,7 @@ Inputs are synthetic and resident in HBM before the timed region.
 A "step" is one ``optimizer.step()``: graph replay (momentum + gather ->
 normaliser -> NS5 -> untile) plus the outside-graph WD/LR application.
 
-    python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline] [--reconfigure T]
 
 Prints one JSON line. ``--gpus N`` with N > 1 exits: this build runs on one GPU.
 """
@@ -152,6 +152,42 @@ def time_apply(opt, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
+def time_reconfigure(opt, tile: int, steps: int) -> dict:
+    """reconfigure(tile_size=tile) mid-run: the plan, buffers and graph are
+    dropped; time each of the eager warm-up steps, the step that recaptures
+    the graph, and the replays that follow (wall clock around each step with
+    device synchronisation)."""
+
+    def timed_step() -> float:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        opt.step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+
+    opt.reconfigure(tile_size=tile)
+    eager = [round(timed_step(), 3) for _ in range(opt._cuda_graph_warmup)]
+    capture = round(timed_step(), 3)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        opt.step()
+    torch.cuda.synchronize()
+    replay = (time.perf_counter() - t0) * 1e3 / steps
+    ns_ms = time_ns_stage(opt, reps=max(3, steps // 2))
+    flops = algorithmic_flops(opt)
+    return {
+        "tile_size": tile,
+        "tiles": sum(g["tiles"].n_tiles for g in opt._groups),
+        "eager_steps_ms": eager,
+        "capture_step_ms": capture,
+        "replay_step_ms": round(replay, 3),
+        "ns5_ms": round(ns_ms, 3),
+        "ns5_tflops": round(flops / (ns_ms * 1e-3) / 1e12, 1),
+        "ns5_frac_peak": round(flops / (ns_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+    }
+
+
 def cpu_baseline(layers, shapes, tile, budget_s: float = 20.0):
     """The CPU oracle (numpy, bf16-staged NS5) on a bounded sample of the same
     workload: the matrices of one layer (or as many of its tiles as fit the time
@@ -218,6 +254,9 @@ def main():
     ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--reconfigure", type=int, default=None, metavar="T",
+                    help="after the timed steps, reconfigure(tile_size=T) and time the eager "
+                         "warm-up steps, the recapture step and the replays of the new regime")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -314,6 +353,8 @@ def main():
             "traffic_frac_hbm_peak": round(traffic / (ns_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if traffic else None,
         },
     }
+    if args.reconfigure:
+        out["reconfigure"] = time_reconfigure(opt, args.reconfigure, args.steps)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(layers, shapes, tile, args.cpu_budget)
     print(json.dumps(out), flush=True)
