@@ -116,9 +116,8 @@ int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_params,
 int himuon_tile_scale(const float* partials, int partials_per_tile,
                       int64_t n_tiles, float eps, float* inv, void* stream);
 
-/* Workspace bytes himuon_ns5 needs for a given sub-batch size (the A and B
- * intermediates of `sub_batch` tiles, then the counters of the dataflow
- * kernel variant). */
+/* Workspace bytes himuon_ns5 needs for a given sub-batch size: the bf16 A and
+ * B intermediates (mp x mp each) of `sub_batch` tiles. */
 size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np);
 
 /*
@@ -134,11 +133,13 @@ size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np);
  *     X = bf16(bf16(B X) + a * X)
  *
  * x, y: (n_tiles, mp, np) bf16; X ping-pongs between them, so the result is
- * in x when `steps` is even and in y when it is odd (x is overwritten).
- * Tiles whose mp and np are multiples of 256 run on persistent 256x256-block
- * kernels, others on 128x128-block kernels. Tiles are processed in
- * sub-batches of `sub_batch`; the workspace must hold
- * himuon_ns5_workspace_bytes(sub_batch, mp, np) bytes.
+ * in x when `steps` is even and in y when it is odd (x is overwritten; x and
+ * y must not alias). Tiles with mp == 128 and np <= 256 run all iterations
+ * of a tile inside one workgroup's LDS; tiles whose mp and np are multiples
+ * of 256 run on persistent 256x256-block kernels; other geometries on
+ * 128x128-block kernels. Tiles are processed in sub-batches of `sub_batch`;
+ * the workspace must hold himuon_ns5_workspace_bytes(sub_batch, mp, np)
+ * bytes whenever steps > 0.
  */
 int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles,
                int mp, int np, int steps, float a, float b, float c,

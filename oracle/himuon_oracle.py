@@ -28,7 +28,12 @@ Functions and the reference lines they restate:
                         tests/integration/test_kernels.py:176-198 (every torch
                         op rounds to bf16)
   lr_scale              himuon.py:181-186
-  step                  one optimizer step on a list of params
+  fma32 / round_to      correctly rounded fp32 fma; cast to a param dtype
+  apply_update          WD/LR of himuon.py:215-228 / 333-348 as torch's GPU
+                        kernels evaluate p.mul_(1-lr*wd) then p.add_(u,
+                        alpha=-lr): u rounded to the param dtype, then one
+                        fp32 fma, then rounded
+  step_param            one optimizer step on a list of params
                         (himuon.py:978-1046, 333-348; graph-mode scaling of
                         himuon.py:337-341 / 222-228)
 
@@ -37,7 +42,12 @@ against torch's in-place ops; tile maps against brute-force loops and
 committed integer tables; chunks against their invariants and the survey's
 worked values; ns5_fp64 against its SVD closed form, rank-1 and diagonal
 closed forms, orthogonal invariance and transpose symmetry; ns5_staged and
-ns5_eager against ns5_fp64 (bf16-sized distance) and the singular-value band.
+ns5_eager against ns5_fp64 (bf16-sized distance) and the singular-value band;
+fma32 against exact rational arithmetic; apply_update against torch's CPU ops
+for fp32 params (bit-exact) and, in tests/test_gpu_apply.py, against torch's
+GPU ops for bf16 and fp32 params (each element equals torch's bulk form or its
+remainder form). fp16 params against torch: parity unpinned (no configuration
+uses them).
 """
 
 from __future__ import annotations
