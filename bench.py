@@ -12,7 +12,8 @@ Inputs are synthetic and resident in HBM before the timed region.
 A "step" is one ``optimizer.step()``: graph replay (momentum + gather ->
 normaliser -> NS5 -> untile) plus the outside-graph WD/LR application.
 
-    python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline] [--reconfigure T]
+    python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline] [--no-adamw]
+                   [--reconfigure T]
 
 Prints one JSON line. ``--gpus N`` with N > 1 exits: this build runs on one GPU.
 """
@@ -152,6 +153,59 @@ def time_apply(opt, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
+def time_adamw(reps: int, rows: int = 151936, cols: int = 2560) -> dict:
+    """The AdamW fallback of one step (himuon.py:359-372) for a Qwen3-4B-shaped
+    embedding (151,936 x 2,560, fp32 grads and moments): the fused HIP pass
+    (himuon_adamw_step: read g, m, v, write m, v, update = 24 B per element)
+    against the reference's torch op chain on the same tensors. HIP events on
+    the current stream, the stream both run on."""
+    from himuon_amd.engine import AdamwTables
+
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    g = torch.randn(rows, cols, device="cuda", generator=gen) * 1e-3
+    m, v, u = torch.zeros_like(g), torch.zeros_like(g), torch.empty_like(g)
+    st = torch.zeros((), device="cuda")
+    tables = AdamwTables([(g, m, v, u, st, 0)])
+
+    def fused():
+        tables.run([0.95], [0.95], [1e-8])
+
+    def torch_ops():
+        st.add_(1)
+        m.lerp_(g, 1 - 0.95)
+        v.lerp_(g.square(), 1 - 0.95)
+        bc1 = 1 - 0.95**st
+        bc2 = 1 - 0.95**st
+        return (m / bc1) / (v.sqrt() / bc2**0.5 + 1e-8)
+
+    def timeit(fn) -> float:
+        s = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        fn()
+        torch.cuda.synchronize()
+        e0.record(s)
+        for _ in range(reps):
+            fn()
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    fused_ms = timeit(fused)
+    torch_ms = timeit(torch_ops)
+    n = g.numel()
+    del g, m, v, u, st, tables
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"Qwen3-4B embed_tokens {rows}x{cols}, fp32 grads and moments",
+        "elements": n,
+        "fused_ms": round(fused_ms, 3),
+        "fused_gbs": round(24.0 * n / (fused_ms * 1e-3) / 1e9, 1),
+        "torch_ops_ms": round(torch_ms, 3),
+        "speedup": round(torch_ms / fused_ms, 2),
+    }
+
+
 def time_reconfigure(opt, tile: int, steps: int) -> dict:
     """reconfigure(tile_size=tile) mid-run: the plan, buffers and graph are
     dropped; time each of the eager warm-up steps, the step that recaptures
@@ -253,6 +307,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-adamw", action="store_true",
+                    help="skip the AdamW fallback timing (Qwen3-4B embedding, fused vs torch ops)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--reconfigure", type=int, default=None, metavar="T",
                     help="after the timed steps, reconfigure(tile_size=T) and time the eager "
@@ -355,6 +411,8 @@ def main():
     }
     if args.reconfigure:
         out["reconfigure"] = time_reconfigure(opt, args.reconfigure, args.steps)
+    if not args.no_adamw:
+        out["adamw"] = time_adamw(reps=max(3, args.steps // 2))
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(layers, shapes, tile, args.cpu_budget)
     print(json.dumps(out), flush=True)

@@ -69,6 +69,26 @@ class ApplyDesc(ctypes.Structure):
 assert ctypes.sizeof(ApplyDesc) == 40
 APPLY_MAX_GROUPS = 32
 
+
+class AdamwDesc(ctypes.Structure):
+    """Mirror of HimuonAdamwDesc (include/himuon_hip.h)."""
+
+    _fields_ = [
+        ("grad", c_void_p),
+        ("moment1", c_void_p),
+        ("moment2", c_void_p),
+        ("update", c_void_p),
+        ("step", c_void_p),
+        ("numel", c_int64),
+        ("chunk0", c_int64),
+        ("group", c_int32),
+        ("reserved", c_int32),
+    ]
+
+
+assert ctypes.sizeof(AdamwDesc) == 64
+ADAMW_MAX_GROUPS = 32
+
 # name -> (restype, argtypes)
 _SIGNATURES = {
     "himuon_abi_version": (c_int, []),
@@ -108,6 +128,12 @@ _SIGNATURES = {
         c_int,
         [c_void_p, c_int, c_int64, c_int, c_int, ctypes.POINTER(c_float), ctypes.POINTER(c_float), c_int,
          c_void_p],
+    ),
+    "himuon_adamw_chunk_elems": (c_int64, []),
+    "himuon_adamw_step": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+         ctypes.POINTER(ctypes.c_double), c_int, c_void_p, c_void_p],
     ),
 }
 
@@ -317,5 +343,31 @@ def apply_updates(desc_table, n_descs, n_chunks, param_dtype, update_dtype, scal
 
 def apply_desc_table(descs: list[ApplyDesc], device) -> torch.Tensor:
     arr = (ApplyDesc * len(descs))(*descs)
+    host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
+    return host.to(device)
+
+
+def adamw_chunk_elems() -> int:
+    return int(load().himuon_adamw_chunk_elems())
+
+
+def adamw_step(desc_table, n_descs, n_chunks, dtype, beta1s, beta2s, epss, bias):
+    """One AdamW fallback step over a descriptor table (himuon.py:359-372):
+    per-group betas/eps are host Python floats; ``bias`` is fp32 device
+    scratch of 2 * n_descs elements."""
+    n = len(beta1s)
+    b1 = (ctypes.c_double * n)(*beta1s)
+    b2 = (ctypes.c_double * n)(*beta2s)
+    ep = (ctypes.c_double * n)(*epss)
+    _check(
+        load().himuon_adamw_step(
+            desc_table.data_ptr(), n_descs, n_chunks, DTYPE_CODES[dtype], b1, b2, ep, n, bias.data_ptr(), _stream()
+        ),
+        "himuon_adamw_step",
+    )
+
+
+def adamw_desc_table(descs: list[AdamwDesc], device) -> torch.Tensor:
+    arr = (AdamwDesc * len(descs))(*descs)
     host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
     return host.to(device)

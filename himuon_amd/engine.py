@@ -181,6 +181,50 @@ class ApplyTables:
             nat.apply_updates(table, n, n_chunks, pdt, udt, scales, alphas)
 
 
+class AdamwTables:
+    """Device descriptor tables for the AdamW fallback step of a list of
+    (grad, moment1, moment2, update, step, group_idx), one table (and one
+    launch pair) per grad dtype, built once: every pointer must stay put, as
+    the graph path requires of grads anyway. Entries the kernel cannot take
+    (non-contiguous, misaligned, mixed or other dtypes, more than
+    ADAMW_MAX_GROUPS groups) are returned in ``fallback`` for the reference's
+    torch ops."""
+
+    def __init__(self, entries):
+        chunk = nat.adamw_chunk_elems()
+        by_dtype: dict[torch.dtype, list] = {}
+        self.fallback = []
+        for e in entries:
+            g, m, v, u, st, gi = e
+            ts = (g, m, v, u)
+            ok = (
+                all(t.is_cuda and t.is_contiguous() and t.data_ptr() % 16 == 0 and t.dtype == g.dtype
+                    and t.numel() == g.numel() for t in ts)
+                and g.dtype in nat.DTYPE_CODES and st.is_cuda and st.dtype == torch.float32 and st.numel() == 1
+                and g.numel() > 0 and gi < nat.ADAMW_MAX_GROUPS
+            )
+            if ok:
+                by_dtype.setdefault(g.dtype, []).append(e)
+            else:
+                self.fallback.append(e)
+        self.launches = []  # (table, n_descs, n_chunks, dtype, bias scratch)
+        for dt, lst in by_dtype.items():
+            descs, c0 = [], 0
+            for g, m, v, u, st, gi in lst:
+                d = nat.AdamwDesc()
+                d.grad, d.moment1, d.moment2, d.update = g.data_ptr(), m.data_ptr(), v.data_ptr(), u.data_ptr()
+                d.step, d.numel, d.chunk0, d.group = st.data_ptr(), g.numel(), c0, gi
+                descs.append(d)
+                c0 += -(-g.numel() // chunk)
+            dev = lst[0][0].device
+            bias = torch.zeros(2 * len(descs), device=dev, dtype=torch.float32)
+            self.launches.append((nat.adamw_desc_table(descs, dev), len(descs), c0, dt, bias))
+
+    def run(self, beta1s: list[float], beta2s: list[float], epss: list[float]) -> None:
+        for table, n, n_chunks, dt, bias in self.launches:
+            nat.adamw_step(table, n, n_chunks, dt, beta1s, beta2s, epss, bias)
+
+
 def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     """Batched NS5 of ``G`` (..., M, N) on the HIP path; same shape and dtype.
 

@@ -29,7 +29,7 @@ import torch
 from torch.optim import Optimizer
 
 from .. import _native as nat
-from ..engine import ApplyTables, TileGroup
+from ..engine import AdamwTables, ApplyTables, TileGroup
 from ..engine import newton_schulz as _hip_newton_schulz
 
 try:
@@ -103,6 +103,11 @@ class HiMuon(Optimizer):
         # (param, update_tensor, group_idx), filled at capture, applied after replay.
         self._pending_updates: list[tuple] = []
         self._apply_tables: "ApplyTables | None" = None  # device tables for _pending_updates
+        # Fused AdamW fallback: persistent update buffers and device tables,
+        # rebuilt when the set of (param, grad storage) changes.
+        self._adamw_updates: dict = {}
+        self._adamw_tables: "AdamwTables | None" = None
+        self._adamw_sig: "tuple | None" = None
 
         # Device state of the HIP path, rebuilt after reconfigure().
         self._groups: "list[dict] | None" = None  # tiled buckets + full-NS shape groups
@@ -153,6 +158,8 @@ class HiMuon(Optimizer):
         self._graph_step_count = 0
         self._pending_updates.clear()
         self._apply_tables = None
+        self._adamw_tables = None
+        self._adamw_sig = None
 
     def _apply_pending_updates(self):
         """WD + LR application after replay, reading the current group lr/wd:
@@ -234,6 +241,8 @@ class HiMuon(Optimizer):
             p.data.add_(update, alpha=-lr)
 
     def _step_adamw(self, group, group_idx):
+        """The reference's per-parameter torch ops (himuon.py:878-888); used
+        for the parameters the fused kernel cannot take."""
         lr = group["lr"]
         weight_decay = group["weight_decay"]
         for p in group["params"]:
@@ -241,6 +250,67 @@ class HiMuon(Optimizer):
                 continue
             update = self._compute_adamw_step(p, p.grad, group["adamw_betas"], group["adamw_eps"])
             self._apply_wd_and_update(p, update, weight_decay, lr, group_idx)
+
+    def _prepare_adamw(self):
+        """State (as the reference creates it: fp32 device step, zero moments in
+        the grad dtype), persistent update buffers and the device tables of the
+        fused AdamW step for every AdamW-group parameter with a grad. Runs
+        outside graph capture; returns the list of (param, group_idx)."""
+        params = []
+        for group_idx, group in enumerate(self.param_groups):
+            if group["use_muon"]:
+                continue
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                g = p.grad
+                st = self.state[p]
+                if "step" not in st:
+                    st["step"] = torch.zeros((), device=g.device)
+                    st["moment1"] = torch.zeros_like(g)
+                    st["moment2"] = torch.zeros_like(g)
+                u = self._adamw_updates.get(p)
+                if u is None or u.shape != g.shape or u.dtype != g.dtype or u.device != g.device:
+                    u = torch.empty_like(g, memory_format=torch.contiguous_format)
+                    self._adamw_updates[p] = u
+                params.append((p, group_idx))
+        sig = tuple(
+            (id(p), p.grad.data_ptr(), p.grad.dtype, self.state[p]["moment1"].data_ptr(),
+             self._adamw_updates[p].data_ptr(), gi)
+            for p, gi in params
+        )
+        if sig != self._adamw_sig:
+            self._adamw_sig = sig
+            entries = [
+                (p.grad, self.state[p]["moment1"], self.state[p]["moment2"], self._adamw_updates[p],
+                 self.state[p]["step"], gi)
+                for p, gi in params
+            ]
+            self._adamw_tables = AdamwTables(entries) if entries else None
+        return params
+
+    def _step_adamw_groups(self):
+        """AdamW fallback groups (himuon.py:1013/1034 -> 878-888): one fused
+        HIP pass per grad dtype (himuon_adamw_step) computes step, moments and
+        the update of every parameter; the update then takes the same WD/LR
+        path as the reference's (deferred to after replay in graph mode)."""
+        params = self._prepare_adamw()
+        if not params:
+            return
+        tables = self._adamw_tables
+        fallback = {e[0].data_ptr() for e in tables.fallback} if tables is not None else set()
+        if tables is not None and tables.launches:
+            b1 = [float(g["adamw_betas"][0]) for g in self.param_groups]
+            b2 = [float(g["adamw_betas"][1]) for g in self.param_groups]
+            ep = [float(g["adamw_eps"]) for g in self.param_groups]
+            tables.run(b1, b2, ep)
+        for p, gi in params:
+            group = self.param_groups[gi]
+            if p.grad.data_ptr() in fallback:
+                update = self._compute_adamw_step(p, p.grad, group["adamw_betas"], group["adamw_eps"])
+            else:
+                update = self._adamw_updates[p]
+            self._apply_wd_and_update(p, update, group["weight_decay"], group["lr"], gi)
 
     # -- Chunk cap and plan (himuon.py:376-415, 459-586) ---------------------
 
@@ -491,9 +561,7 @@ class HiMuon(Optimizer):
             raise NotImplementedError("HiMuon (HIP path) runs on one GPU; FSDP/DTensor parameters are not supported")
         groups = self._ensure_device_state()
         stats = self._run_groups(groups) if groups else {"ns_gpu_ms": 0.0, "ns_launches": 0, "total_B": 0}
-        for group_idx, group in enumerate(self.param_groups):
-            if not group["use_muon"]:
-                self._step_adamw(group, group_idx)
+        self._step_adamw_groups()
         n = stats["ns_launches"]
         self._last_step_stats = {
             "ns_gpu_ms": float(stats["ns_gpu_ms"]),
@@ -514,6 +582,7 @@ class HiMuon(Optimizer):
     def _capture_graph(self) -> None:
         """Capture momentum..untile into a hipGraph; WD/LR stay outside."""
         self._ensure_device_state()  # allocate everything before capture
+        self._prepare_adamw()
         torch.cuda.synchronize()
         self._pending_updates.clear()
         self._apply_tables = None

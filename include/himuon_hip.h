@@ -191,6 +191,44 @@ int himuon_apply_updates(const HimuonApplyDesc* descs_dev, int n_descs,
                          const float* alpha_by_group, int n_groups,
                          void* stream);
 
+/*
+ * AdamW fallback step for the parameters of the non-Muon groups, inside the
+ * captured step (replaces _compute_adamw_step, himuon.py:359-372, called from
+ * _step_adamw, himuon.py:878-888). One descriptor per parameter, in device
+ * memory; grad, moment1, moment2 and update are contiguous, 16-byte aligned
+ * and of one dtype (`dtype`, the grad dtype); step points at the parameter's
+ * fp32 step counter. Descriptor d owns chunks [chunk0_d, chunk0_d +
+ * ceil(numel_d / himuon_adamw_chunk_elems())). For each parameter:
+ *     step += 1; bc1 = 1 - powf(b1, step); sbc2 = sqrtf(1 - powf(b2, step))
+ * and for each element (rd = round to dtype, fp32 arithmetic):
+ *     m = rd(lerp(m, g, 1 - b1)); v = rd(lerp(v, rd(g*g), 1 - b2))
+ *     update = rd(rd(m / rd(bc1)) / rd(rd(rd(sqrt(v)) / rd(sbc2)) + eps))
+ * lerp as torch evaluates it (one fma). beta1/beta2/eps are HOST arrays of
+ * n_groups doubles (the Python floats; 1 - beta is formed in double and then
+ * rounded, as the reference's lerp weight is). bias_dev is device scratch of
+ * 2 * n_descs floats that receives (bc1, sbc2) per descriptor.
+ */
+#define HIMUON_ADAMW_MAX_GROUPS 32
+
+typedef struct HimuonAdamwDesc {
+  const void* grad;   /* contiguous gradient                                */
+  void* moment1;      /* contiguous first moment (exp_avg), updated in place */
+  void* moment2;      /* contiguous second moment, updated in place          */
+  void* update;       /* contiguous output                                   */
+  float* step;        /* fp32 step counter of this parameter (device)        */
+  int64_t numel;
+  int64_t chunk0;     /* first chunk of this parameter in the launch          */
+  int32_t group;      /* index into the per-group hyper-parameter arrays      */
+  int32_t reserved;
+} HimuonAdamwDesc;
+
+int64_t himuon_adamw_chunk_elems(void);
+
+int himuon_adamw_step(const HimuonAdamwDesc* descs_dev, int n_descs,
+                      int64_t n_chunks, int dtype, const double* beta1_by_group,
+                      const double* beta2_by_group, const double* eps_by_group,
+                      int n_groups, float* bias_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

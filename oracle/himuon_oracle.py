@@ -33,6 +33,9 @@ Functions and the reference lines they restate:
                         kernels evaluate p.mul_(1-lr*wd) then p.add_(u,
                         alpha=-lr): u rounded to the param dtype, then one
                         fp32 fma, then rounded
+  lerp32 / adamw_bias / adamw_step
+                        AdamW fallback step, himuon.py:359-372 (torch's lerp
+                        as an fma; every op rounded to the moment dtype)
   step_param            one optimizer step on a list of params
                         (himuon.py:978-1046, 333-348; graph-mode scaling of
                         himuon.py:337-341 / 222-228)
@@ -47,7 +50,13 @@ fma32 against exact rational arithmetic; apply_update against torch's CPU ops
 for fp32 params (bit-exact) and, in tests/test_gpu_apply.py, against torch's
 GPU ops for bf16 and fp32 params (each element equals torch's bulk form or its
 remainder form). fp16 params against torch: parity unpinned (no configuration
-uses them).
+uses them). lerp32 against torch's CPU lerp (both weight branches,
+bit-exact); adamw_step against torch's CPU ops: bf16 moments and update and
+fp32 moments bit-exact (torch's CPU fp32 sqrt is not correctly rounded, so
+the fp32 update is pinned within 2 ulp there), adamw_bias against its
+float64 closed form; on the GPU (tests/test_gpu_adamw.py) the kernel's
+moments and update equal adamw_step given the kernel's bias corrections, and
+the kernel equals torch's GPU ops bit for bit.
 """
 
 from __future__ import annotations
@@ -348,6 +357,63 @@ def apply_update(p, update, lr: float, wd: float, dtype: str = "float32") -> np.
         p = round_to(p * F32(1 - lr * wd), dtype)
     u = round_to(np.asarray(update, dtype=F32), dtype)
     return round_to(fma32(F32(-lr), u, p), dtype)
+
+
+# ---------------------------------------------------------------------------
+# AdamW fallback (himuon.py:359-372, 878-888)
+# ---------------------------------------------------------------------------
+def lerp32(a, b, w) -> np.ndarray:
+    """torch's lerp with a scalar weight in fp32 opmath: fma(w, b - a, a) for
+    |w| < 0.5, else fma(-(b - a), 1 - w, b) (the form torch's kernels take;
+    ATen Lerp.h, is_lerp_weight_small)."""
+    a = np.asarray(a, dtype=F32)
+    b = np.asarray(b, dtype=F32)
+    w = F32(w)
+    d = (b - a).astype(F32)
+    if abs(float(w)) < 0.5:
+        return fma32(w, d, a)
+    return fma32(-d, F32(1) - w, b)
+
+
+def adamw_bias(beta: float, step) -> F32:
+    """1 - beta ** step in fp32 with a correctly rounded pow (step is the
+    fp32 counter after its increment). The reference evaluates the power with
+    the device math library's powf, which is not correctly rounded: it may
+    differ from this in the last bit at some steps."""
+    pw = F32(np.float64(F32(beta)) ** np.float64(F32(step)))
+    return F32(F32(1) - pw)
+
+
+def adamw_step(g, m, v, step, betas, eps, dtype: str = "float32", bias=None):
+    """One AdamW fallback step (himuon.py:359-372) as torch's GPU kernels
+    evaluate it, every op's result stored in the moment dtype (= grad dtype):
+
+        step += 1
+        m = lerp(m, g, 1 - b1); v = lerp(v, g*g, 1 - b2)
+        update = (m / bc1) / (sqrt(v) / sqrt(bc2) + eps)
+
+    1 - beta is formed in double (a Python float) and then rounded to fp32, as
+    the lerp weight is. bc1 and sqrt(bc2) are fp32 0-dim tensors there, which
+    the GPU kernels cast to the moment dtype before dividing (a CPU scalar
+    operand would keep fp32); the Python-float eps enters in fp32. ``bias`` =
+    (bc1, sqrt(bc2)) overrides the bias corrections (for a comparison that
+    takes them from the device). Returns (update, m, v, step, (bc1,
+    sqrt(bc2))) with the fp32 bias corrections."""
+    b1, b2 = betas
+    s = F32(F32(step) + F32(1))
+    g = round_to(np.asarray(g, dtype=F32), dtype)
+    m = round_to(lerp32(m, g, F32(1.0 - b1)), dtype)
+    v = round_to(lerp32(v, round_to(g * g, dtype), F32(1.0 - b2)), dtype)
+    if bias is None:
+        bc1 = adamw_bias(b1, s)
+        sbc2 = np.sqrt(adamw_bias(b2, s), dtype=F32)
+    else:
+        bc1, sbc2 = F32(bias[0]), F32(bias[1])
+    t1 = round_to(m / round_to(bc1, dtype), dtype)
+    t2 = round_to(np.sqrt(v, dtype=F32), dtype)
+    t3 = round_to(round_to(t2 / round_to(sbc2, dtype), dtype) + F32(eps), dtype)
+    u = round_to(t1 / t3, dtype)
+    return u, m, v, s, (bc1, sbc2)
 
 
 @dataclass

@@ -56,6 +56,30 @@ def test_desc_layout_matches_header():
     assert d.mu.offset == 84 and d.nesterov.offset == 88
 
 
+def test_adamw_desc_layout_matches_header():
+    # offsets of HimuonAdamwDesc fields (include/himuon_hip.h)
+    d = nat.AdamwDesc
+    assert ctypes.sizeof(d) == 64
+    assert d.update.offset == 24 and d.step.offset == 32 and d.numel.offset == 40
+    assert d.chunk0.offset == 48 and d.group.offset == 56
+    a = nat.ApplyDesc
+    assert ctypes.sizeof(a) == 40 and a.chunk0.offset == 24 and a.group.offset == 32
+
+
+def test_adamw_argument_errors(lib):
+    z = None
+    one = (ctypes.c_double * 1)(0.95)
+    many = (ctypes.c_double * 40)(*([0.95] * 40))
+    assert lib.himuon_adamw_chunk_elems() > 0
+    # null descriptor table or bias scratch
+    assert lib.himuon_adamw_step(z, 1, 4, 0, one, one, one, 1, 8, z) == -22
+    assert lib.himuon_adamw_step(8, 1, 4, 0, one, one, one, 1, z, z) == -22
+    # unknown dtype code, too many groups, missing host arrays
+    assert lib.himuon_adamw_step(8, 1, 4, 9, one, one, one, 1, 8, z) == -22
+    assert lib.himuon_adamw_step(8, 1, 4, 0, many, many, many, 40, 8, z) == -22
+    assert lib.himuon_adamw_step(8, 1, 4, 0, z, one, one, 1, 8, z) == -22
+
+
 def test_partials_per_tile(lib):
     assert lib.himuon_gather_partials_per_tile(512, 512, 512, 512) == 512 // 32  # 32-row slabs
     assert lib.himuon_gather_partials_per_tile(256, 1024, 256, 1024) == 256 // 32

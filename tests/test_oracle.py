@@ -110,6 +110,133 @@ def test_apply_update_weight_decay_matches_torch_mul(dtype, tdt):
     assert np.array_equal(got, ref.float().numpy())
 
 
+# ---------------------------------------------------------------------------
+# AdamW fallback (himuon.py:359-372)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("w", [0.05, 1e-3, 0.5, 0.7])
+def test_lerp32_matches_torch_lerp(w):
+    """torch's CPU lerp_ with a scalar weight equals lerp32 bit for bit in
+    both branches (|w| < 0.5: fma(w, b-a, a); else fma(-(b-a), 1-w, b)); the
+    separately rounded forms differ on this sample."""
+    rng = np.random.default_rng(11)
+    a = (rng.standard_normal(200001) * 1e-3).astype(np.float32)
+    b = (rng.standard_normal(200001) * 1e-3).astype(np.float32)
+    ref = torch.from_numpy(a.copy()).lerp_(torch.from_numpy(b), w).numpy()
+    assert np.array_equal(O.lerp32(a, b, w), ref)
+    if w == 0.5:  # d * (1 - w) is exact: both forms agree
+        return
+    wf, d = np.float32(w), (b - a).astype(np.float32)
+    if w < 0.5:
+        sep = (a + (wf * d).astype(np.float32)).astype(np.float32)
+    else:
+        sep = (b - (d * (np.float32(1) - wf)).astype(np.float32)).astype(np.float32)
+    assert not np.array_equal(sep, ref)
+
+
+def test_adamw_bias_closed_form():
+    """adamw_bias = 1 - beta**step with the power correctly rounded to fp32:
+    checked against a float64 evaluation with an error bound (the float64
+    power is within 2^-50 relative, so the fp32 rounding is decided unless the
+    exact value is that close to a rounding boundary), and exact for step 1."""
+    for beta in (0.95, 0.9, 0.999):
+        bf = np.float64(np.float32(beta))
+        assert O.adamw_bias(beta, 1) == np.float32(np.float32(1) - np.float32(beta))
+        for s in range(1, 400):
+            exact = bf ** s
+            lo, hi = np.float32(exact * (1 - 2**-50)), np.float32(exact * (1 + 2**-50))
+            if lo == hi:  # rounding decided
+                assert O.adamw_bias(beta, s) == np.float32(np.float32(1) - lo)
+
+
+def _torch_adamw(g, m, v, step, betas, eps):
+    """The reference's _compute_adamw_step body (himuon.py:366-372) on CPU
+    tensors. On the GPU the fp32 0-dim bias corrections are cast to the
+    moment dtype before the divisions (TensorIterator's common-dtype cast);
+    torch's CPU kernels treat a 0-dim operand as an fp32 scalar instead, so
+    the cast is written out here to reproduce the GPU semantics."""
+    step.add_(1)
+    m.lerp_(g, 1 - betas[0])
+    v.lerp_(g.square(), 1 - betas[1])
+    bc1 = (1 - betas[0] ** step).to(m.dtype)
+    bc2 = 1 - betas[1] ** step
+    return (m / bc1) / (v.sqrt() / (bc2**0.5).to(m.dtype) + eps)
+
+
+def test_adamw_step_bf16_matches_torch_ops():
+    """bf16 moments: the whole chain over 5 steps equals torch's CPU ops bit
+    for bit (every op's result rounded to bf16)."""
+    rng = np.random.default_rng(12)
+    n, betas, eps = 65537, (0.95, 0.9), 1e-8
+    step = torch.zeros(())
+    m = torch.zeros(n, dtype=torch.bfloat16)
+    v = torch.zeros(n, dtype=torch.bfloat16)
+    om = np.zeros(n, np.float32)
+    ov = np.zeros(n, np.float32)
+    os_ = np.float32(0)
+    for _ in range(5):
+        g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32)).to(torch.bfloat16)
+        u = _torch_adamw(g, m, v, step, betas, eps)
+        ou, om, ov, os_, _ = O.adamw_step(g.float().numpy(), om, ov, os_, betas, eps, "bfloat16")
+        assert np.array_equal(om, m.float().numpy())
+        assert np.array_equal(ov, v.float().numpy())
+        assert np.array_equal(ou, u.float().numpy())
+        assert os_ == step.item()
+
+
+def test_adamw_step_fp32_matches_torch_ops():
+    """fp32 moments equal torch's CPU ops bit for bit over 5 steps. torch's CPU
+    fp32 sqrt is not correctly rounded (numpy's is; about 0.7% of these
+    inputs differ by 1 ulp), and the error carries through the division, the
+    eps add and the quotient, so the update is pinned here within 8 ulp on
+    under 2% of elements, and bit for bit against torch's GPU ops
+    (tests/test_gpu_adamw.py)."""
+    rng = np.random.default_rng(13)
+    n, betas, eps = 65537, (0.95, 0.95), 1e-8
+    step = torch.zeros(())
+    m = torch.zeros(n)
+    v = torch.zeros(n)
+    om = np.zeros(n, np.float32)
+    ov = np.zeros(n, np.float32)
+    os_ = np.float32(0)
+    for _ in range(5):
+        g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32))
+        u = _torch_adamw(g, m, v, step, betas, eps)
+        ou, om, ov, os_, _ = O.adamw_step(g.numpy(), om, ov, os_, betas, eps, "float32")
+        assert np.array_equal(om, m.numpy())
+        assert np.array_equal(ov, v.numpy())
+        ulp = np.abs(ou.view(np.int32).astype(np.int64) - u.numpy().view(np.int32).astype(np.int64))
+        assert ulp.max() <= 8
+        assert np.count_nonzero(ulp) < 0.02 * n
+
+
+def test_adamw_step_closed_form_first_step():
+    """From zero moments, step 1 gives m = w1 g and v = w2 g^2 (w = fp32 of
+    1 - beta formed in double) and bc = 1 - fp32(beta), so without
+    intermediate rounding update = (g w1/bc1) / (|g| sqrt(w2/bc2) + eps). The
+    fp32 constants make w/bc differ from 1 by up to 1.3e-5 (beta 0.999), which
+    the oracle must reproduce; a planted mistake in a weight, a bias
+    correction or the eps placement breaks the match by far more than a few
+    ulp."""
+    rng = np.random.default_rng(14)
+    g = (rng.standard_normal(10000) * 1e-3).astype(np.float32)
+    z = np.zeros_like(g)
+    for betas in ((0.95, 0.95), (0.9, 0.999)):
+        u, m, v, s, (bc1, sbc2) = O.adamw_step(g, z, z, 0, betas, 1e-8)
+        w1, w2 = (np.float64(np.float32(1.0 - b)) for b in betas)
+        c1, c2 = (np.float64(np.float32(1) - np.float32(b)) for b in betas)
+        g64 = g.astype(np.float64)
+        expect = (g64 * w1 / c1) / (np.abs(g64) * np.sqrt(w2 / c2) + 1e-8)
+        assert s == 1
+        assert np.max(np.abs(u - expect)) < 6e-7
+        naive = g64 / (np.abs(g64) + 1e-8)  # the textbook value, off by the fp32 constants
+        if betas[1] == 0.999:
+            assert np.max(np.abs(u - naive)) > 5e-6
+    # eps inside the square root instead of outside changes the answer
+    u, *_ = O.adamw_step(g, z, z, 0, (0.95, 0.95), 1e-4)
+    wrong = g / np.sqrt(g.astype(np.float64) ** 2 + 1e-4)
+    assert np.max(np.abs(u - wrong)) > 1e-3
+
+
 def test_fma32_is_correctly_rounded():
     """fma32 against exact rational arithmetic, including cancellation and
     halfway cases that a float64 evaluation would double-round."""
