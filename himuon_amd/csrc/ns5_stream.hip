@@ -22,10 +22,15 @@
 //
 // MFMA operands are swapped (A operand = rows j, B operand = rows i), so lane
 // l holds C[row l%32][4 consecutive columns]. The epilogue converts in
-// registers, stages each wave's 128x128 bf16 result in its own 32 KiB of LDS
-// and writes it with 16-byte row-contiguous stores (256 bytes per row). Off-
-// diagonal Gram blocks also write the mirrored block: a 4x4 transpose across
-// each lane quad (two DPP exchanges) restages the sub-block as rows of C^T.
+// registers, then first issues the workgroup's next item's first 4 K units
+// into ring slots 0..3, so that their latency, and the drain of this item's
+// stores (vmcnt retires loads and stores in issue order), overlap this
+// epilogue instead of stalling the next item's start. It then stages each
+// wave's 128x128 bf16 result through its 8 KiB quarter of ring slot 4, in 4
+// rounds of 32 rows, and writes it with 16-byte row-contiguous stores (256
+// bytes per row). Off-diagonal Gram blocks also write the mirrored block: a
+// 4x4 transpose across each lane quad (two DPP exchanges) restages the
+// sub-block as rows of C^T.
 #include "ns5_kernels.h"
 
 namespace {
@@ -89,12 +94,22 @@ HM_DEV int swz_p(int r) { return (((r >> 1) ^ (r >> 3)) & 1) | (((r >> 2) & 1) <
 HM_DEV int swz_x(int r) { return 10 * (r & 1) + 4 * ((r >> 1) & 1); }
 HM_DEV int swz_c(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
-// vmcnt while waiting for unit w: loads of the (up to DIST - 1) units issued
-// after it. A K unit is L loads per wave, an R unit 8.
+// vmcnt while waiting for unit w: the loads of the (up to DIST - 1) units
+// issued after it (a K unit is L loads per wave, an R unit 8) and, when this
+// item's first DIST units were prefetched during the previous item's
+// epilogue, the sp global stores of that epilogue, which were issued after
+// unit DIST - 1 and before unit DIST (vmcnt counts loads and stores together
+// and retires them in issue order). sp is 0, 32 or 64; with 64 the count is
+// capped at the counter's maximum, which waits for slightly more than needed.
 template <int L, int NR>
-HM_DEV void wait_unit(int nk, int w) {
+HM_DEV void wait_unit(int nk, int w, int sp) {
   const int rem = nk - 1 - w;
-  if (rem >= 3) {
+  if (w < DIST && sp > 0) {  // nk >= 8, so rem >= 4 here
+    if (sp > 32)
+      wait_vm<63>();
+    else
+      wait_vm<3 * L + 32>();
+  } else if (rem >= 3) {
     wait_vm<3 * L>();
   } else if (rem == 2) {
     wait_vm<2 * L + (NR >= 1 ? 8 : 0)>();
@@ -105,13 +120,78 @@ HM_DEV void wait_unit(int nk, int w) {
   }
 }
 
+// Item position: output block (bi, bj) of one tile.
+struct ItemPos {
+  int64_t tile;
+  int bi, bj;
+  bool diag;  // Gram diagonal block (Q = P, no mirror)
+};
+
+// Per-lane global sources of an item's P and Q operand units.
+struct ItemSrc {
+  const uint16_t* p;
+  const uint16_t* q;
+  int64_t pstep, qstep, qunit;
+};
+
+template <int MODE>
+HM_DEV ItemSrc item_src(const StArgs& g, const ItemPos& it, int lane, int wave) {
+  // Row panel (256 rows x 64 B): wave instruction n = 4 i + wave fills rows
+  // 16 n .. 16 n + 15; lane l lands at row 16 n + l/4, position l%4 and
+  // fetches chunk (l%4) ^ swz_p(row) (row & 15 = l/4).
+  const int prl = lane >> 2;
+  const int pch = (lane & 3) ^ swz_p(prl);
+  ItemSrc s;
+  s.p = g.P + it.tile * g.p_bs + (int64_t)(it.bi * BT + 16 * wave + prl) * g.ldp + pch * 8;
+  s.pstep = 64 * (int64_t)g.ldp;
+  if constexpr (MODE == kApply) {
+    // X panel (32 k-rows x 512 B): instruction n fills k-rows 2n, 2n + 1;
+    // lane l lands at row 2n + l/32, position l%32, fetching chunk
+    // (l%32) ^ swz_x(row) (row & 3 = (2 wave + hi) & 3).
+    const int xr = 2 * wave + (lane >> 5);
+    const int xc = (lane & 31) ^ swz_x(xr);
+    s.q = g.Q + it.tile * g.q_bs + (int64_t)xr * g.ldq + it.bj * BT + xc * 8;
+    s.qstep = 8 * (int64_t)g.ldq;
+    s.qunit = BK * (int64_t)g.ldq;
+  } else {
+    s.q = g.Q + it.tile * g.q_bs + (int64_t)(it.bj * BT + 16 * wave + prl) * g.ldq + pch * 8;
+    s.qstep = 64 * (int64_t)g.ldq;
+    s.qunit = BK;
+  }
+  return s;
+}
+
+// K unit v of an item into ring slot `slot` (wdst = the wave's 1 KiB part).
+HM_DEV void issue_k(const ItemSrc& s, uint32_t wdst, int v, int slot, bool diag) {
+  const uint32_t d = wdst + slot * SLOT;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    dma16(s.p + i * s.pstep + v * BK, d + i * 4096);
+  if (!diag) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(s.q + i * s.qstep + v * s.qunit, d + HALF + i * 4096);
+  }
+}
+
 // One 256x256 output block C[tile][bi-block][bj-block]. DIAG: Gram diagonal
 // block, Q = P (one panel streamed), no mirror.
+//
+// pre_st: 0 if this item's first DIST units are still to be issued, else the
+// number of global stores (32 or 64) the previous item's epilogue issued
+// after prefetching them. nx: the next item of this workgroup (if `more`); its
+// first DIST units are issued into ring slots 0..DIST-1 as soon as this
+// item no longer needs the ring, before this item's stores, so that neither
+// their latency nor the store drain is exposed at the next item's start.
+// Returns the number of global stores issued by this item's epilogue.
 template <int MODE, bool DIAG, int NKC>
-__device__ __forceinline__ void st_item(const StArgs& g, lds_u8* lds, int64_t tile, int bi, int bj) {
+__device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemPos it, int pre_st,
+                                       const bool more, const ItemPos nx) {
   constexpr bool kTr = MODE == kApply;
   constexpr int NR = (MODE == kGramA) ? 0 : 4;  // R units
   constexpr int L = DIAG ? 4 : 8;               // K-unit loads per wave
+  const int64_t tile = it.tile;
+  const int bi = it.bi, bj = it.bj;
   // The lane index is made opaque per block so that the per-lane addresses
   // below are recomputed for each block instead of being hoisted out of the
   // persistent loop (where they would not fit in registers).
@@ -124,29 +204,7 @@ __device__ __forceinline__ void st_item(const StArgs& g, lds_u8* lds, int64_t ti
   const int U = nk + NR;
 
   // ---- loaders ------------------------------------------------------------
-  // Row panel (256 rows x 64 B): wave instruction n = 4 i + wave fills rows
-  // 16 n .. 16 n + 15; lane l lands at row 16 n + l/4, position l%4 and
-  // fetches chunk (l%4) ^ swz_p(row) (row & 15 = l/4).
-  const int prl = lane >> 2;
-  const int pch = (lane & 3) ^ swz_p(prl);
-  const uint16_t* psrc = g.P + tile * g.p_bs + (int64_t)(bi * BT + 16 * wave + prl) * g.ldp + pch * 8;
-  const int64_t pstep = 64 * (int64_t)g.ldp;
-  const uint16_t* qsrc;
-  int64_t qstep, qunit;
-  if constexpr (kTr) {
-    // X panel (32 k-rows x 512 B): instruction n fills k-rows 2n, 2n + 1;
-    // lane l lands at row 2n + l/32, position l%32, fetching chunk
-    // (l%32) ^ swz_x(row) (row & 3 = (2 wave + hi) & 3).
-    const int xr = 2 * wave + hi;
-    const int xc = l32 ^ swz_x(xr);
-    qsrc = g.Q + tile * g.q_bs + (int64_t)xr * g.ldq + bj * BT + xc * 8;
-    qstep = 8 * (int64_t)g.ldq;
-    qunit = BK * (int64_t)g.ldq;
-  } else {
-    qsrc = g.Q + tile * g.q_bs + (int64_t)(bj * BT + 16 * wave + prl) * g.ldq + pch * 8;
-    qstep = 64 * (int64_t)g.ldq;
-    qunit = BK;
-  }
+  const ItemSrc src = item_src<MODE>(g, it, lane, wave);
   // R unit q (block rows 64 q .. 64 q + 63, 256 columns, 512-byte rows):
   // instruction n = 4 i + wave fills rows 2n, 2n + 1; chunk (l%32) ^ (row & 15).
   const uint16_t* rsrc = nullptr;
@@ -155,17 +213,11 @@ __device__ __forceinline__ void st_item(const StArgs& g, lds_u8* lds, int64_t ti
   const uint32_t wdst = (uint32_t)(uintptr_t)lds + wave * 1024;
 
   auto issue = [&](int v) {
-    const uint32_t d = wdst + (v % NSLOT) * SLOT;
+    const int slot = v % NSLOT;
     if (v < nk) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dma16(psrc + i * pstep + v * BK, d + i * 4096);
-      if constexpr (!DIAG) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          dma16(qsrc + i * qstep + v * qunit, d + HALF + i * 4096);
-      }
+      issue_k(src, wdst, v, slot, DIAG);
     } else if constexpr (NR > 0) {
+      const uint32_t d = wdst + slot * SLOT;
       const int q = v - nk;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -228,11 +280,13 @@ __device__ __forceinline__ void st_item(const StArgs& g, lds_u8* lds, int64_t ti
   // frees slot u % NSLOT (every wave has its unit-u fragments in registers),
   // which receives unit u + 1 + DIST. The second half of unit u's MFMAs runs
   // after the barrier, covering the first fragment reads of unit u + 1.
-  lds_barrier();  // the previous block's epilogue is done with the LDS
+  if (pre_st == 0) {
+    lds_barrier();  // the previous block's epilogue is done with the LDS
 #pragma unroll
-  for (int v = 0; v < DIST; ++v) issue(v);
-  wait_unit<L, NR>(nk, 0);
-  lds_barrier();
+    for (int v = 0; v < DIST; ++v) issue(v);
+  }
+  wait_unit<L, NR>(nk, 0, pre_st);
+  lds_barrier();  // unit 0 is in; every wave is past the previous epilogue's staging
   issue(DIST);
   u32x4_t fa0[4], fb0[4], fa1[4], fb1[4];
   // At most one half-unit of fragment reads is in flight at any time (8 or 12
@@ -248,7 +302,7 @@ __device__ __forceinline__ void st_item(const StArgs& g, lds_u8* lds, int64_t ti
     mma(fa0, fb0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm<0>();  // second-half fragments of unit u
-    wait_unit<L, NR>(nk, u + 1);
+    wait_unit<L, NR>(nk, u + 1, pre_st);
     lds_barrier();
     if (u + 1 + DIST < U) issue(u + 1 + DIST);
     frags(u + 1, 0, fa0, fb0);
@@ -312,50 +366,67 @@ __device__ __forceinline__ void st_item(const StArgs& g, lds_u8* lds, int64_t ti
           out[ti][tj][q] = u32x2_t{pk_bf16(v[4 * q], v[4 * q + 1]), pk_bf16(v[4 * q + 2], v[4 * q + 3])};
         }
   }
-  lds_barrier();  // all fragment and R reads are done: the LDS is free for staging
+  lds_barrier();  // all fragment and R reads are done: the ring is free
 
-  // Stage the wave's 128x128 sub-block (256-byte rows, chunk ^ swz_c(row)),
-  // then store it with 16-byte lanes, 4 rows x 256 bytes per instruction.
-  lds_u8* const W = lds + wave * SLOT;
-  const int srow = lane >> 4, sch = lane & 15;
-  auto store_stage = [&](uint16_t* dst, int ld) {
-    wait_lgkm<0>();
+  // The next item's first DIST units go to ring slots 0..DIST-1 now, ahead
+  // of this item's stores; slot DIST is the staging area.
+  if (more) {
+    const ItemSrc ns = item_src<MODE>(g, nx, lane, wave);
 #pragma unroll
-    for (int n = 0; n < 32; ++n) {
+    for (int v = 0; v < DIST; ++v) issue_k(ns, wdst, v, v, nx.diag);
+  }
+
+  // Staging in 4 rounds per block: each wave stages 32 rows x 128 columns
+  // (8 KiB, 256-byte rows, chunk ^ swz_c(row)) in its quarter of slot DIST,
+  // then stores them with 16-byte lanes, 4 rows x 256 bytes per instruction:
+  // 8 stores per round, 32 per block. LDS operations of one wave execute in
+  // order, so a round's writes may follow the previous round's reads without
+  // a wait.
+  lds_u8* const W = lds + DIST * SLOT + wave * 8192;
+  const int srow = lane >> 4, sch = lane & 15;
+  auto store_round = [&](uint16_t* dst, int ld) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
       const int r = 4 * n + srow;
       const u32x4_t v = *reinterpret_cast<lds_cu32x4*>(W + r * 256 + ((sch ^ swz_c(r)) * 16));
       *reinterpret_cast<u32x4_t*>(dst + (int64_t)r * ld + sch * 8) = v;
     }
   };
+  uint16_t* Ct = g.C + tile * g.c_bs;
+  uint16_t* const cdst = Ct + (int64_t)(bi * BT + wm * 128) * g.ldc + bj * BT + wn * 128;
 #pragma unroll
-  for (int ti = 0; ti < 4; ++ti)
+  for (int ti = 0; ti < 4; ++ti) {
 #pragma unroll
     for (int tj = 0; tj < 4; ++tj)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int r = 32 * ti + l32, ch = 4 * tj + q;
-        *reinterpret_cast<lds_u32x2*>(W + r * 256 + ((ch ^ swz_c(r)) * 16) + hi * 8) = out[ti][tj][q];
+        const int ch = 4 * tj + q;
+        *reinterpret_cast<lds_u32x2*>(W + l32 * 256 + ((ch ^ swz_c(l32)) * 16) + hi * 8) = out[ti][tj][q];
       }
-  uint16_t* Ct = g.C + tile * g.c_bs;
-  store_stage(Ct + (int64_t)(bi * BT + wm * 128) * g.ldc + bj * BT + wn * 128, g.ldc);
+    store_round(cdst + (int64_t)(32 * ti) * g.ldc, g.ldc);
+  }
+  int stores = 32;
   if constexpr (MODE != kApply && !DIAG) {
     // Mirror block (bj, bi): after the quad transpose, lane (a = l32/4,
     // k = l32%4) holds C^T[jt][it..it+3], jt = 32 tj + 8 q + 4 hi + k,
-    // it = 32 ti + 4 a (wave-local).
-    wait_lgkm<0>();  // this wave's staging reads are done
+    // it = 32 ti + 4 a (wave-local); round tj stages rows 32 tj .. 32 tj + 31.
+    uint16_t* const mdst = Ct + (int64_t)(bj * BT + wn * 128) * g.ldc + bi * BT + wm * 128;
     const int k = lane & 3, a = l32 >> 2;
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
+    for (int tj = 0; tj < 4; ++tj) {
 #pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
+      for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const u32x2_t tv = quad_transpose(out[ti][tj][q], k);
-          const int r = 32 * tj + 8 * q + 4 * hi + k, ch = 4 * ti + (a >> 1);
+          const int r = 8 * q + 4 * hi + k, ch = 4 * ti + (a >> 1);
           *reinterpret_cast<lds_u32x2*>(W + r * 256 + ((ch ^ swz_c(r)) * 16) + (a & 1) * 8) = tv;
         }
-    store_stage(Ct + (int64_t)(bj * BT + wn * 128) * g.ldc + bi * BT + wm * 128, g.ldc);
+      store_round(mdst + (int64_t)(32 * tj) * g.ldc, g.ldc);
+    }
+    stores = 64;
   }
+  return stores;
 }
 
 // NKC: K units known at compile time (16: K = 512, the tile_size 512 case;
@@ -370,21 +441,37 @@ __global__ __launch_bounds__(NT, 1) void ns_st_kernel(StArgs g) {
   const int64_t per_xcd = (total + 7) >> 3;
   const int64_t ibeg = (int64_t)(blockIdx.x & 7) * per_xcd;
   const int64_t iend = (ibeg + per_xcd < total) ? ibeg + per_xcd : total;
-  for (int64_t item = ibeg + (blockIdx.x >> 3); item < iend; item += wper) {
-    const int64_t tile = item / per_tile;
-    const int p = (int)(item - tile * per_tile);
+  auto pos = [&](int64_t item) {
+    ItemPos q;
+    q.tile = item / per_tile;
+    const int p = (int)(item - q.tile * per_tile);
     if constexpr (MODE == kApply) {
-      const int bi = p / nbj;
-      st_item<MODE, false, NKC>(g, (lds_u8*)lds, tile, bi, p - bi * nbj);
+      q.bi = p / nbj;
+      q.bj = p - q.bi * nbj;
+      q.diag = false;
     } else {
       int bi = 0;
       while ((bi + 1) * (bi + 2) / 2 <= p) ++bi;
-      const int bj = p - bi * (bi + 1) / 2;
-      if (bi == bj)
-        st_item<MODE, true, NKC>(g, (lds_u8*)lds, tile, bi, bj);
-      else
-        st_item<MODE, false, NKC>(g, (lds_u8*)lds, tile, bi, bj);
+      q.bi = bi;
+      q.bj = p - bi * (bi + 1) / 2;
+      q.diag = q.bi == q.bj;
     }
+    return q;
+  };
+  int64_t item = ibeg + (blockIdx.x >> 3);
+  if (item >= iend) return;
+  ItemPos cur = pos(item);
+  int pre_st = 0;
+  for (;;) {
+    const int64_t next = item + wper;
+    const bool more = next < iend;
+    const ItemPos nxt = pos(more ? next : item);
+    const int st = cur.diag ? st_item<MODE, true, NKC>(g, (lds_u8*)lds, cur, pre_st, more, nxt)
+                            : st_item<MODE, false, NKC>(g, (lds_u8*)lds, cur, pre_st, more, nxt);
+    if (!more) break;
+    pre_st = st;
+    item = next;
+    cur = nxt;
   }
 }
 
