@@ -48,10 +48,13 @@ def ns_path() -> str:
 
 PEAK_HBM_GBS = 8000.0
 
-# HBM bytes the NS5 stage moves per step, from rocprofv3 --pmc FETCH_SIZE /
-# WRITE_SIZE (scaled by a 256 MiB copy of known size) on this config; see
-# profiles/himuon_step_qwen3-4b_t512.md. Other configs: not measured (null).
-NS5_STAGE_TRAFFIC_BYTES = {"qwen3-4b": 321.69e9}
+# HBM bytes the NS5 stage moves per step, measured with rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE on this config, each scaled by what the counter
+# reads for this script's 256 MiB device copy (FETCH_SIZE x 1.9995, WRITE_SIZE
+# x 1.0): per 3,465-tile dispatch GramA reads 1.865 GB, GramB 2.769 GB, Apply
+# 4.827 GB, the X0 scaling 1.816 GB, each writing 1.817 GB; 20 + 20 + 20 + 4
+# dispatches per step. Other configs: not measured (null).
+NS5_STAGE_TRAFFIC_BYTES = {"qwen3-4b": 312.75e9}
 
 CONFIGS = {
     # name: (layers, [(h, w) per layer], tile_size, param dtype, description)
