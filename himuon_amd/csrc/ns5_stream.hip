@@ -241,11 +241,15 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   const int tr_row = 8 * hi + te;
   const int tr_chunk = wn * 16 + 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
   const int tr_sub = (r16 & 1) * 8;
-  auto frags = [&](int v, int ks, u32x4_t(&fa)[4], u32x4_t(&fb)[4]) {
+  // which: 1 = P fragments (fb), 2 = Q fragments (fa), 3 = both.
+  auto frags = [&](int v, int ks, u32x4_t(&fa)[4], u32x4_t(&fb)[4], int which = 3) {
     const lds_u8* s = lds + (v % NSLOT) * SLOT;
     const int pos = ((2 * ks + hi) ^ sp) * 16;
+    if (which & 1) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) fb[t] = *reinterpret_cast<lds_cu32x4*>(s + prow + t * 2048 + pos);
+      for (int t = 0; t < 4; ++t) fb[t] = *reinterpret_cast<lds_cu32x4*>(s + prow + t * 2048 + pos);
+    }
+    if (!(which & 2)) return;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       if constexpr (kTr) {
@@ -273,6 +277,10 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) acc[tj][ti] = mfma(fa[tj], fb[ti], acc[tj][ti]);
   };
+  auto mma_row = [&](const u32x4_t(&fa)[4], const u32x4_t(&fb)[4], int tj) {
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) acc[tj][ti] = mfma(fa[tj], fb[ti], acc[tj][ti]);
+  };
 
   // ---- K loop ------------------------------------------------------------------
   // Unit u lives in slot u % NSLOT. At the top of unit u + 1 each wave waits
@@ -298,16 +306,28 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   __builtin_amdgcn_sched_barrier(0);
   frags(0, 1, fa1, fb1);
   __builtin_amdgcn_sched_barrier(0);
+  // After the barrier, the DMA issue of unit u + 1 + DIST and the first-half
+  // fragment reads of unit u + 1 go between the rows of unit u's second-half
+  // MFMAs, so that they issue while the MFMA pipe is busy.
   auto unit = [&](int u) {
     mma(fa0, fb0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm<0>();  // second-half fragments of unit u
     wait_unit<L, NR>(nk, u + 1, pre_st);
     lds_barrier();
-    if (u + 1 + DIST < U) issue(u + 1 + DIST);
-    frags(u + 1, 0, fa0, fb0);
+    mma_row(fa1, fb1, 0);
     __builtin_amdgcn_sched_barrier(0);
-    mma(fa1, fb1);
+    if (u + 1 + DIST < U) issue(u + 1 + DIST);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_row(fa1, fb1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    frags(u + 1, 0, fa0, fb0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_row(fa1, fb1, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    frags(u + 1, 0, fa0, fb0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_row(fa1, fb1, 3);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm<0>();  // first-half fragments of unit u + 1
     frags(u + 1, 1, fa1, fb1);
