@@ -6,9 +6,12 @@
 //   Apply : C = X' = bf16(bf16(B X) + a X) P = B (rows, K = m), Q = X read as [k][j]
 // (ns5_smem.py:89-101, XXT.py:55-75, ba_plus_cAA.py:58-85, fused_bmm_add.py:65-88).
 //
-// One 256-thread workgroup per CU (4 waves in 2x2, each a 128x128 sub-block
-// of 4x4 v_mfma_f32_32x32x16_bf16 tiles, 256 fp32 accumulators per lane)
-// walks a contiguous range of output blocks of its XCD.
+// One workgroup per CU walks a contiguous range of output blocks of its XCD:
+// 8 waves in 2x4, two per SIMD, each a 128x64 sub-block of 4x2
+// v_mfma_f32_32x32x16_bf16 tiles (128 fp32 accumulators per lane), so that
+// one wave's MFMAs run while the other on its SIMD waits at a barrier or
+// issues loads. (The code also takes 4 waves in 2x2 of 128x128 each, one
+// per SIMD; that layout measured slower.)
 //
 // Operand stream. K advances in units of 32. Each unit of P (and Q) goes
 // straight from global memory into a 32 KiB slot of a 5-slot LDS ring
@@ -95,28 +98,31 @@ HM_DEV int swz_x(int r) { return 10 * (r & 1) + 4 * ((r >> 1) & 1); }
 HM_DEV int swz_c(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 // vmcnt while waiting for unit w: the loads of the (up to DIST - 1) units
-// issued after it (a K unit is L loads per wave, an R unit 8) and, when this
+// issued after it (a K unit is L loads per wave, an R unit RL) and, when this
 // item's first DIST units were prefetched during the previous item's
 // epilogue, the sp global stores of that epilogue, which were issued after
 // unit DIST - 1 and before unit DIST (vmcnt counts loads and stores together
-// and retires them in issue order). sp is 0, 32 or 64; with 64 the count is
-// capped at the counter's maximum, which waits for slightly more than needed.
-template <int L, int NR>
+// and retires them in issue order). sp is 0, 16, 32 or 64; with 64 the count
+// is capped at the counter's maximum, which waits for slightly more than
+// needed.
+template <int L, int NR, int RL>
 HM_DEV void wait_unit(int nk, int w, int sp) {
   const int rem = nk - 1 - w;
-  if (w < DIST && sp > 0) {  // nk >= 8, so rem >= 4 here
+  if (w < DIST && sp > 0) {  // nk >= 8, so rem >= 4 here; sp is 16, 32 or 64
     if (sp > 32)
       wait_vm<63>();
+    else if (sp == 16)
+      wait_vm<3 * L + 16>();
     else
       wait_vm<3 * L + 32>();
   } else if (rem >= 3) {
     wait_vm<3 * L>();
   } else if (rem == 2) {
-    wait_vm<2 * L + (NR >= 1 ? 8 : 0)>();
+    wait_vm<2 * L + (NR >= 1 ? RL : 0)>();
   } else if (rem == 1) {
-    wait_vm<L + (NR >= 2 ? 16 : 8 * NR)>();
+    wait_vm<L + (NR >= 2 ? 2 * RL : RL * NR)>();
   } else {
-    wait_vm<(NR >= 3 ? 24 : 8 * NR)>();
+    wait_vm<(NR >= 3 ? 3 * RL : RL * NR)>();
   }
 }
 
@@ -134,16 +140,17 @@ struct ItemSrc {
   int64_t pstep, qstep, qunit;
 };
 
-template <int MODE>
+// NW waves per workgroup share each unit's 32 one-KiB load instructions.
+template <int MODE, int NW>
 HM_DEV ItemSrc item_src(const StArgs& g, const ItemPos& it, int lane, int wave) {
-  // Row panel (256 rows x 64 B): wave instruction n = 4 i + wave fills rows
+  // Row panel (256 rows x 64 B): wave instruction n = NW i + wave fills rows
   // 16 n .. 16 n + 15; lane l lands at row 16 n + l/4, position l%4 and
   // fetches chunk (l%4) ^ swz_p(row) (row & 15 = l/4).
   const int prl = lane >> 2;
   const int pch = (lane & 3) ^ swz_p(prl);
   ItemSrc s;
   s.p = g.P + it.tile * g.p_bs + (int64_t)(it.bi * BT + 16 * wave + prl) * g.ldp + pch * 8;
-  s.pstep = 64 * (int64_t)g.ldp;
+  s.pstep = 16 * NW * (int64_t)g.ldp;
   if constexpr (MODE == kApply) {
     // X panel (32 k-rows x 512 B): instruction n fills k-rows 2n, 2n + 1;
     // lane l lands at row 2n + l/32, position l%32, fetching chunk
@@ -151,26 +158,27 @@ HM_DEV ItemSrc item_src(const StArgs& g, const ItemPos& it, int lane, int wave) 
     const int xr = 2 * wave + (lane >> 5);
     const int xc = (lane & 31) ^ swz_x(xr);
     s.q = g.Q + it.tile * g.q_bs + (int64_t)xr * g.ldq + it.bj * BT + xc * 8;
-    s.qstep = 8 * (int64_t)g.ldq;
+    s.qstep = 2 * NW * (int64_t)g.ldq;
     s.qunit = BK * (int64_t)g.ldq;
   } else {
     s.q = g.Q + it.tile * g.q_bs + (int64_t)(it.bj * BT + 16 * wave + prl) * g.ldq + pch * 8;
-    s.qstep = 64 * (int64_t)g.ldq;
+    s.qstep = 16 * NW * (int64_t)g.ldq;
     s.qunit = BK;
   }
   return s;
 }
 
 // K unit v of an item into ring slot `slot` (wdst = the wave's 1 KiB part).
+template <int NW>
 HM_DEV void issue_k(const ItemSrc& s, uint32_t wdst, int v, int slot, bool diag) {
   const uint32_t d = wdst + slot * SLOT;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    dma16(s.p + i * s.pstep + v * BK, d + i * 4096);
+  for (int i = 0; i < 16 / NW; ++i)
+    dma16(s.p + i * s.pstep + v * BK, d + i * NW * 1024);
   if (!diag) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma16(s.q + i * s.qstep + v * s.qunit, d + HALF + i * 4096);
+    for (int i = 0; i < 16 / NW; ++i)
+      dma16(s.q + i * s.qstep + v * s.qunit, d + HALF + i * NW * 1024);
   }
 }
 
@@ -184,12 +192,21 @@ HM_DEV void issue_k(const ItemSrc& s, uint32_t wdst, int v, int slot, bool diag)
 // item no longer needs the ring, before this item's stores, so that neither
 // their latency nor the store drain is exposed at the next item's start.
 // Returns the number of global stores issued by this item's epilogue.
-template <int MODE, bool DIAG, int NKC>
+//
+// NW = 4: waves in 2 x 2, each a 128x128 sub-block (4x4 MFMA tiles, 256
+// accumulators per lane, one wave per SIMD). NW = 8: waves in 2 x 4, each
+// 128x64 (4x2 tiles, 128 accumulators, two waves per SIMD, so that one
+// wave's MFMAs can run while the other waits or issues loads).
+template <int MODE, bool DIAG, int NKC, int NW>
 __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemPos it, int pre_st,
                                        const bool more, const ItemPos nx) {
   constexpr bool kTr = MODE == kApply;
-  constexpr int NR = (MODE == kGramA) ? 0 : 4;  // R units
-  constexpr int L = DIAG ? 4 : 8;               // K-unit loads per wave
+  constexpr int NR = (MODE == kGramA) ? 0 : 4;   // R units
+  constexpr int WN = NW / 2;                      // waves along the block's columns
+  constexpr int WC = BT / WN;                     // columns per wave (128 or 64)
+  constexpr int TJ = WC / 32;                     // MFMA tiles along a wave's columns
+  constexpr int L = (DIAG ? 16 : 32) / NW;        // K-unit loads per wave
+  constexpr int RL = 32 / NW;                     // R-unit loads per wave
   const int64_t tile = it.tile;
   const int bi = it.bi, bj = it.bj;
   // The lane index is made opaque per block so that the per-lane addresses
@@ -198,15 +215,15 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int l32 = lane & 31, hi = lane >> 5;
   const int nk = NKC > 0 ? NKC : g.K / BK;  // K units (compile-time for the common K)
   const int U = nk + NR;
 
   // ---- loaders ------------------------------------------------------------
-  const ItemSrc src = item_src<MODE>(g, it, lane, wave);
+  const ItemSrc src = item_src<MODE, NW>(g, it, lane, wave);
   // R unit q (block rows 64 q .. 64 q + 63, 256 columns, 512-byte rows):
-  // instruction n = 4 i + wave fills rows 2n, 2n + 1; chunk (l%32) ^ (row & 15).
+  // instruction n = NW i + wave fills rows 2n, 2n + 1; chunk (l%32) ^ (row & 15).
   const uint16_t* rsrc = nullptr;
   if constexpr (NR > 0)
     rsrc = g.R + tile * g.r_bs + (int64_t)(bi * BT + 2 * wave + hi) * g.ldr + bj * BT;
@@ -215,15 +232,15 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   auto issue = [&](int v) {
     const int slot = v % NSLOT;
     if (v < nk) {
-      issue_k(src, wdst, v, slot, DIAG);
+      issue_k<NW>(src, wdst, v, slot, DIAG);
     } else if constexpr (NR > 0) {
       const uint32_t d = wdst + slot * SLOT;
       const int q = v - nk;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int sw = 8 * (i & 1) + 2 * wave + hi;  // (64 q + 8 i + 2 wave + hi) & 15
-        const uint16_t* s = rsrc + (int64_t)(64 * q + 8 * i) * g.ldr + ((l32 ^ sw) * 8);
-        dma16(s, d + i * 4096);
+      for (int i = 0; i < RL; ++i) {
+        const int sw = (2 * NW * i + 2 * wave + hi) & 15;  // row & 15
+        const uint16_t* s = rsrc + (int64_t)(64 * q + 2 * NW * i) * g.ldr + ((l32 ^ sw) * 8);
+        dma16(s, d + i * NW * 1024);
       }
     }
   };
@@ -233,16 +250,16 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   // operand: the same from Q (rows j) for Gram; for Apply two transposing
   // reads of the X panel (ds_read_b64_tr_b16: within 16 lanes, lane 4a+b
   // receives element b of the 8-byte rows addressed by lanes a, a+4, a+8,
-  // a+12), giving lane l column j = wn*128 + 32 t + l%32, k = 16 ks + 8 hi + 0..7.
+  // a+12), giving lane l column j = wn*WC + 32 t + l%32, k = 16 ks + 8 hi + 0..7.
   const int sp = swz_p(l32 & 15);
-  const int prow = (wm * 128 + l32) * 64, qrow = (wn * 128 + l32) * 64;
+  const int prow = (wm * 128 + l32) * 64, qrow = (wn * WC + l32) * 64;
   const int r16 = lane & 15, te = r16 >> 2;
   const int tr_s = swz_x(te);
   const int tr_row = 8 * hi + te;
-  const int tr_chunk = wn * 16 + 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
+  const int tr_chunk = wn * (WC / 8) + 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
   const int tr_sub = (r16 & 1) * 8;
   // which: 1 = P fragments (fb), 2 = Q fragments (fa), 3 = both.
-  auto frags = [&](int v, int ks, u32x4_t(&fa)[4], u32x4_t(&fb)[4], int which = 3) {
+  auto frags = [&](int v, int ks, u32x4_t(&fa)[TJ], u32x4_t(&fb)[4], int which = 3) {
     const lds_u8* s = lds + (v % NSLOT) * SLOT;
     const int pos = ((2 * ks + hi) ^ sp) * 16;
     if (which & 1) {
@@ -251,7 +268,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     }
     if (!(which & 2)) return;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < TJ; ++t) {
       if constexpr (kTr) {
         const uint32_t off = (uint32_t)(uintptr_t)s + HALF + (16 * ks + tr_row) * 512 +
                              (((tr_chunk + 4 * t) ^ tr_s) * 16) + tr_sub;
@@ -264,20 +281,20 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     }
   };
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[TJ][4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < TJ; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
-  auto mma = [&](const u32x4_t(&fa)[4], const u32x4_t(&fb)[4]) {
+  auto mma = [&](const u32x4_t(&fa)[TJ], const u32x4_t(&fb)[4]) {
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj)
+    for (int tj = 0; tj < TJ; ++tj)
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) acc[tj][ti] = mfma(fa[tj], fb[ti], acc[tj][ti]);
   };
-  auto mma_row = [&](const u32x4_t(&fa)[4], const u32x4_t(&fb)[4], int tj) {
+  auto mma_row = [&](const u32x4_t(&fa)[TJ], const u32x4_t(&fb)[4], int tj) {
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) acc[tj][ti] = mfma(fa[tj], fb[ti], acc[tj][ti]);
   };
@@ -293,10 +310,10 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
 #pragma unroll
     for (int v = 0; v < DIST; ++v) issue(v);
   }
-  wait_unit<L, NR>(nk, 0, pre_st);
+  wait_unit<L, NR, RL>(nk, 0, pre_st);
   lds_barrier();  // unit 0 is in; every wave is past the previous epilogue's staging
   issue(DIST);
-  u32x4_t fa0[4], fb0[4], fa1[4], fb1[4];
+  u32x4_t fa0[TJ], fb0[4], fa1[TJ], fb1[4];
   // At most one half-unit of fragment reads is in flight at any time (8 or 12
   // LDS operations: lgkmcnt counts to 15). Unit u: the first-half fragments
   // have landed at its start and the second-half reads are in flight; each
@@ -313,7 +330,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     mma(fa0, fb0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm<0>();  // second-half fragments of unit u
-    wait_unit<L, NR>(nk, u + 1, pre_st);
+    wait_unit<L, NR, RL>(nk, u + 1, pre_st);
     lds_barrier();
     mma_row(fa1, fb1, 0);
     __builtin_amdgcn_sched_barrier(0);
@@ -323,11 +340,13 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     __builtin_amdgcn_sched_barrier(0);
     frags(u + 1, 0, fa0, fb0, 1);
     __builtin_amdgcn_sched_barrier(0);
-    mma_row(fa1, fb1, 2);
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (TJ > 2) {
+      mma_row(fa1, fb1, 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     frags(u + 1, 0, fa0, fb0, 2);
     __builtin_amdgcn_sched_barrier(0);
-    mma_row(fa1, fb1, 3);
+    if constexpr (TJ > 3) mma_row(fa1, fb1, 3);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm<0>();  // first-half fragments of unit u + 1
     frags(u + 1, 1, fa1, fb1);
@@ -346,8 +365,8 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
 
   // ---- epilogue ------------------------------------------------------------------
   // out[ti][tj][q] = 4 bf16 of C[i][j..j+3], i = wm*128 + 32 ti + l32,
-  // j = wn*128 + 32 tj + 8 q + 4 hi (block-local).
-  u32x2_t out[4][4][4];
+  // j = wn*WC + 32 tj + 8 q + 4 hi (block-local).
+  u32x2_t out[4][TJ][4];
   if constexpr (NR > 0) {
     wait_vm<0>();
     lds_barrier();  // every wave's R loads have landed
@@ -357,10 +376,10 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
       const int rq = il & 63;
       const lds_u8* rs = lds + ((nk + (il >> 6)) % NSLOT) * SLOT + rq * 512 + hi * 8;
 #pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
+      for (int tj = 0; tj < TJ; ++tj)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int ch = wn * 16 + 4 * tj + q;
+          const int ch = wn * (WC / 8) + 4 * tj + q;
           const u32x2_t rv = *reinterpret_cast<lds_cu32x2*>(rs + ((ch ^ (rq & 15)) * 16));
           float y[4];
 #pragma unroll
@@ -379,7 +398,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
+      for (int tj = 0; tj < TJ; ++tj)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const f32x16_t& v = acc[tj][ti];
@@ -391,68 +410,83 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   // The next item's first DIST units go to ring slots 0..DIST-1 now, ahead
   // of this item's stores; slot DIST is the staging area.
   if (more) {
-    const ItemSrc ns = item_src<MODE>(g, nx, lane, wave);
+    const ItemSrc ns = item_src<MODE, NW>(g, nx, lane, wave);
 #pragma unroll
-    for (int v = 0; v < DIST; ++v) issue_k(ns, wdst, v, v, nx.diag);
+    for (int v = 0; v < DIST; ++v) issue_k<NW>(ns, wdst, v, v, nx.diag);
   }
 
-  // Staging in 4 rounds per block: each wave stages 32 rows x 128 columns
-  // (8 KiB, 256-byte rows, chunk ^ swz_c(row)) in its quarter of slot DIST,
-  // then stores them with 16-byte lanes, 4 rows x 256 bytes per instruction:
-  // 8 stores per round, 32 per block. LDS operations of one wave execute in
-  // order, so a round's writes may follow the previous round's reads without
-  // a wait.
-  lds_u8* const W = lds + DIST * SLOT + wave * 8192;
-  const int srow = lane >> 4, sch = lane & 15;
-  auto store_round = [&](uint16_t* dst, int ld) {
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      const int r = 4 * n + srow;
-      const u32x4_t v = *reinterpret_cast<lds_cu32x4*>(W + r * 256 + ((sch ^ swz_c(r)) * 16));
-      *reinterpret_cast<u32x4_t*>(dst + (int64_t)r * ld + sch * 8) = v;
-    }
-  };
+  // Staging in 4 rounds per block: each wave stages 32 rows x WC columns
+  // (WC * 2-byte rows) in its 1/NW of slot DIST, then stores them with
+  // 16-byte lanes, whole rows per instruction: 8 (NW = 4) or 4 (NW = 8)
+  // stores per round. LDS operations of one wave execute in order, so a
+  // round's writes may follow the previous round's reads without a wait.
+  // Row swizzle: 256-byte rows chunk ^ swz_c(row); 128-byte rows (two per
+  // 256-byte bank line) chunk ^ ((row >> 1) & 7).
+  constexpr int RB = WC * 2, CPR = WC / 8, RPI = 64 / CPR;
+  lds_u8* const W = lds + DIST * SLOT + wave * (SLOT / NW);
+  auto swz_s = [](int r) { return CPR == 16 ? swz_c(r) : ((r >> 1) & 7); };
   uint16_t* Ct = g.C + tile * g.c_bs;
-  uint16_t* const cdst = Ct + (int64_t)(bi * BT + wm * 128) * g.ldc + bj * BT + wn * 128;
+  uint16_t* const cdst = Ct + (int64_t)(bi * BT + wm * 128) * g.ldc + bj * BT + wn * WC;
+  {
+    const int srow = lane / CPR, sch = lane % CPR;
 #pragma unroll
-  for (int ti = 0; ti < 4; ++ti) {
+    for (int ti = 0; ti < 4; ++ti) {
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj)
+      for (int tj = 0; tj < TJ; ++tj)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int ch = 4 * tj + q;
-        *reinterpret_cast<lds_u32x2*>(W + l32 * 256 + ((ch ^ swz_c(l32)) * 16) + hi * 8) = out[ti][tj][q];
+        for (int q = 0; q < 4; ++q) {
+          const int ch = 4 * tj + q;
+          *reinterpret_cast<lds_u32x2*>(W + l32 * RB + ((ch ^ swz_s(l32)) * 16) + hi * 8) = out[ti][tj][q];
+        }
+      uint16_t* const dst = cdst + (int64_t)(32 * ti) * g.ldc;
+#pragma unroll
+      for (int n = 0; n < 32 / RPI; ++n) {
+        const int r = RPI * n + srow;
+        const u32x4_t v = *reinterpret_cast<lds_cu32x4*>(W + r * RB + ((sch ^ swz_s(r)) * 16));
+        *reinterpret_cast<u32x4_t*>(dst + (int64_t)r * g.ldc + sch * 8) = v;
       }
-    store_round(cdst + (int64_t)(32 * ti) * g.ldc, g.ldc);
+    }
   }
-  int stores = 32;
+  int stores = 4 * (32 / RPI);
   if constexpr (MODE != kApply && !DIAG) {
     // Mirror block (bj, bi): after the quad transpose, lane (a = l32/4,
     // k = l32%4) holds C^T[jt][it..it+3], jt = 32 tj + 8 q + 4 hi + k,
-    // it = 32 ti + 4 a (wave-local); round tj stages rows 32 tj .. 32 tj + 31.
-    uint16_t* const mdst = Ct + (int64_t)(bj * BT + wn * 128) * g.ldc + bi * BT + wm * 128;
+    // it = 32 ti + 4 a (wave-local): 256-byte rows. A round stages MR rows
+    // (32 for NW = 4: all q of one tj; 16 for NW = 8: a pair of q).
+    constexpr int MR = (SLOT / NW) / 256, QR = MR / 8;
+    uint16_t* const mdst = Ct + (int64_t)(bj * BT + wn * WC) * g.ldc + bi * BT + wm * 128;
     const int k = lane & 3, a = l32 >> 2;
+    const int srow = lane >> 4, sch = lane & 15;
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
+    for (int tj = 0; tj < TJ; ++tj) {
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti)
+      for (int q0 = 0; q0 < 4; q0 += QR) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const u32x2_t tv = quad_transpose(out[ti][tj][q], k);
-          const int r = 8 * q + 4 * hi + k, ch = 4 * ti + (a >> 1);
-          *reinterpret_cast<lds_u32x2*>(W + r * 256 + ((ch ^ swz_c(r)) * 16) + (a & 1) * 8) = tv;
+        for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+          for (int qq = 0; qq < QR; ++qq) {
+            const u32x2_t tv = quad_transpose(out[ti][tj][q0 + qq], k);
+            const int r = 8 * qq + 4 * hi + k, ch = 4 * ti + (a >> 1);
+            *reinterpret_cast<lds_u32x2*>(W + r * 256 + ((ch ^ swz_c(r)) * 16) + (a & 1) * 8) = tv;
+          }
+        uint16_t* const dst = mdst + (int64_t)(32 * tj + 8 * q0) * g.ldc;
+#pragma unroll
+        for (int n = 0; n < MR / 4; ++n) {
+          const int r = 4 * n + srow;
+          const u32x4_t v = *reinterpret_cast<lds_cu32x4*>(W + r * 256 + ((sch ^ swz_c(r)) * 16));
+          *reinterpret_cast<u32x4_t*>(dst + (int64_t)r * g.ldc + sch * 8) = v;
         }
-      store_round(mdst + (int64_t)(32 * tj) * g.ldc, g.ldc);
+      }
     }
-    stores = 64;
+    stores += TJ * (4 / QR) * (MR / 4);
   }
   return stores;
 }
 
 // NKC: K units known at compile time (16: K = 512, the tile_size 512 case;
-// 0: K from the arguments).
-template <int MODE, int NKC>
-__global__ __launch_bounds__(NT, 1) void ns_st_kernel(StArgs g) {
+// 0: K from the arguments). NW: waves per workgroup (4 or 8).
+template <int MODE, int NKC, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void ns_st_kernel(StArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
   const int nbi = g.M / BT, nbj = g.N / BT;
   const int per_tile = (MODE == kApply) ? nbi * nbj : nbi * (nbi + 1) / 2;
@@ -486,8 +520,8 @@ __global__ __launch_bounds__(NT, 1) void ns_st_kernel(StArgs g) {
     const int64_t next = item + wper;
     const bool more = next < iend;
     const ItemPos nxt = pos(more ? next : item);
-    const int st = cur.diag ? st_item<MODE, true, NKC>(g, (lds_u8*)lds, cur, pre_st, more, nxt)
-                            : st_item<MODE, false, NKC>(g, (lds_u8*)lds, cur, pre_st, more, nxt);
+    const int st = cur.diag ? st_item<MODE, true, NKC, NW>(g, (lds_u8*)lds, cur, pre_st, more, nxt)
+                            : st_item<MODE, false, NKC, NW>(g, (lds_u8*)lds, cur, pre_st, more, nxt);
     if (!more) break;
     pre_st = st;
     item = next;
@@ -526,10 +560,13 @@ void launch(const StArgs& a, int64_t items, hipStream_t s) {
   const int64_t per_xcd = (items + 7) / 8;
   const int64_t wgs_per_xcd = std::max<int64_t>(1, std::min<int64_t>(num_cus() / 8, per_xcd));
   const dim3 grid((unsigned)(8 * wgs_per_xcd));
+  // 8 waves (two per SIMD): 4.5 % faster than 4 at K = 512 and about 10 %
+  // at K = 256 and 1024 on MI355X, so only that layout is launched.
+  constexpr int kNW = 8;
   if (a.K == 16 * BK)
-    hipLaunchKernelGGL((ns_st_kernel<MODE, 16>), grid, dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((ns_st_kernel<MODE, 16, kNW>), grid, dim3(64 * kNW), 0, s, a);
   else
-    hipLaunchKernelGGL((ns_st_kernel<MODE, 0>), grid, dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((ns_st_kernel<MODE, 0, kNW>), grid, dim3(64 * kNW), 0, s, a);
 }
 
 }  // namespace
