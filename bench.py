@@ -365,6 +365,9 @@ def main():
     n_tiles = sum(g["tiles"].n_tiles for g in opt._groups)
     traffic = NS5_STAGE_TRAFFIC_BYTES.get(args.config) if ns_path() == "stream" else None
     n_el = sum(p.numel() for p in params)
+    # bytes per element: update (untile writes it, the WD/LR pass reads it), parameter
+    ub = torch.empty(0, dtype=opt._groups[0]["tiles"].upd_dtype).element_size()
+    pb = params[0].element_size()
     ns_tflops = flops / (ns_ms * 1e-3) / 1e12
 
     out = {
@@ -397,9 +400,10 @@ def main():
         "gather_ms": round(gather_ms, 3),
         "gather_gbs": round(14.0 * n_el / (gather_ms * 1e-3) / 1e9, 1),
         "untile_ms": round(untile_ms, 3),
-        "untile_gbs": round(6.0 * n_el / (untile_ms * 1e-3) / 1e9, 1),
+        "untile_gbs": round((2 + ub) * n_el / (untile_ms * 1e-3) / 1e9, 1),
         "apply_ms": round(apply_ms, 3),
-        "apply_gbs": round(8.0 * n_el / (apply_ms * 1e-3) / 1e9, 1) if pdtype == torch.bfloat16 else None,
+        "apply_gbs": round((2 * pb + ub) * n_el / (apply_ms * 1e-3) / 1e9, 1),
+        "update_dtype": str(opt._groups[0]["tiles"].upd_dtype).replace("torch.", ""),
         "roofline": {
             "kernel": NS_KERNELS.get(ns_path(), ns_path()),
             "bound": "mfma",

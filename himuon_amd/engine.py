@@ -7,7 +7,8 @@ device, allocated once so pointers stay stable for hipGraph capture:
   himuon.py:588-612, stored directly as the bf16 NS operand) that X
   ping-pongs between,
 * the per-tile sum-of-squares partials and normalisers,
-* the per-parameter ``update`` tensors (grad dtype) the untile kernel writes,
+* the per-parameter ``update`` tensors the untile kernel writes (grad dtype,
+  or the parameters' dtype when that is narrower: see ``update_dtype``),
 * the device descriptor table (HimuonParamDesc[]) the gather/untile kernels read.
 
 ``run()`` issues: momentum+gather -> tile scale -> NS5 per chunk -> untile.
@@ -18,6 +19,20 @@ from __future__ import annotations
 import torch
 
 from . import _native as nat
+
+
+def update_dtype(params, grad_dtype: torch.dtype) -> torch.dtype:
+    """Storage dtype of a group's update tensors. The update's only consumer
+    is the WD/LR application, which (as torch's in-place add does) first rounds
+    it to the parameter dtype; when every parameter of the group has one dtype
+    narrower than fp32 grads, storing the update already rounded to it gives
+    the same parameters bit for bit and moves 2 bytes per element instead of 4."""
+    pdts = {p.dtype for p in params}
+    if grad_dtype == torch.float32 and len(pdts) == 1:
+        (pd,) = pdts
+        if pd in (torch.bfloat16, torch.float16):
+            return pd
+    return grad_dtype
 
 
 class TileGroup:
@@ -33,11 +48,15 @@ class TileGroup:
         nesterovs: list[bool],
         device: torch.device,
         dtype: torch.dtype,
+        upd_dtype: torch.dtype | None = None,
     ):
         self.tile_h, self.tile_w = int(tile_h), int(tile_w)
         self.m, self.n, self.mp, self.np, self.trans = nat.ns_geometry(self.tile_h, self.tile_w)
         self.device = device
-        self.dtype = dtype
+        self.dtype = dtype  # grads and momentum
+        # Update buffers: the grad dtype, or the parameters' own narrower dtype
+        # when the only consumer of the update rounds it to that dtype first.
+        self.upd_dtype = dtype if upd_dtype is None else upd_dtype
         self.params = params
         counts = []
         for g in grads:
@@ -53,7 +72,7 @@ class TileGroup:
         self.alt = torch.empty(shape, device=device, dtype=torch.bfloat16)
         self.partials = torch.empty((self.n_tiles, self.ppt), device=device, dtype=torch.float32)
         self.inv = torch.empty((self.n_tiles,), device=device, dtype=torch.float32)
-        self.updates = [torch.empty(g.shape, device=device, dtype=dtype) for g in grads]
+        self.updates = [torch.empty(g.shape, device=device, dtype=self.upd_dtype) for g in grads]
         self.upd_scales = list(upd_scales)
         self._sig = None
         self.desc = None
@@ -133,7 +152,7 @@ class TileGroup:
     def untile(self, steps: int = 5) -> None:
         nat.untile(
             self.desc, len(self.updates), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
-            self.dtype, self.result(steps),
+            self.upd_dtype, self.result(steps),
         )
 
     def workspace_bytes(self, sub_batch: int) -> int:

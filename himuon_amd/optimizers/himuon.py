@@ -29,7 +29,7 @@ import torch
 from torch.optim import Optimizer
 
 from .. import _native as nat
-from ..engine import AdamwTables, ApplyTables, TileGroup
+from ..engine import AdamwTables, ApplyTables, TileGroup, update_dtype
 from ..engine import newton_schulz as _hip_newton_schulz
 
 try:
@@ -444,6 +444,7 @@ class HiMuon(Optimizer):
                 nesterovs=[e[1]["nesterov"] for e in entries],
                 device=params[0].grad.device,
                 dtype=dtype,
+                upd_dtype=update_dtype(params, dtype),
             )
             self._concat_buffers[bucket["bucket_key"]] = grp.tiles
             out.append(
@@ -472,6 +473,7 @@ class HiMuon(Optimizer):
                 nesterovs=[g["nesterov"] for _, g in entries],
                 device=params[0].grad.device,
                 dtype=dtype,
+                upd_dtype=update_dtype(params, dtype),
             )
             out.append(
                 {

@@ -110,3 +110,39 @@ def test_oracle_apply_matches_torch_gpu(pdt, name, udt):
         _reference(r, u0.to(DEV), lr, wd)
         got = O.apply_update(p0.float().numpy(), u0.float().numpy(), lr, wd, name)
         assert (got == r.float().cpu().numpy()).all(), (name, udt, lr, wd)
+
+
+@pytest.mark.parametrize("pdt", [torch.bfloat16, torch.float16])
+def test_narrow_update_storage_gives_identical_params(pdt):
+    """The optimizer stores a bucket's update in the parameters' dtype when
+    that is narrower than the fp32 grads (engine.update_dtype): the WD/LR
+    pass rounds the update to the parameter dtype first, so parameters must
+    come out bit-identical to the fp32-update path."""
+    from himuon_amd.engine import TileGroup, update_dtype
+
+    gen = torch.Generator().manual_seed(21)
+    shapes = [(1024, 1536), (512, 700), (300, 512)]
+    params = [(torch.randn(*s, generator=gen) * 0.02).to(pdt).to(DEV) for s in shapes]
+    grads = [(torch.randn(*s, generator=gen) * 1e-3).to(DEV) for s in shapes]
+    assert update_dtype(params, torch.float32) == pdt
+    assert update_dtype(params, torch.bfloat16) == torch.bfloat16
+    assert update_dtype([params[0], params[1].float()], torch.float32) == torch.float32
+    results = []
+    for udt in (torch.float32, pdt):
+        moms = [torch.zeros_like(g) for g in grads]
+        grp = TileGroup(params=params, grads=grads, moms=moms, tile_h=512, tile_w=512,
+                        upd_scales=[0.2 * 512**0.5] * 3, mus=[0.95] * 3, nesterovs=[True] * 3,
+                        device=torch.device(DEV), dtype=torch.float32, upd_dtype=udt)
+        ws = torch.empty(grp.workspace_bytes(grp.default_sub_batch()), device=DEV, dtype=torch.uint8)
+        grp.gather()
+        grp.ns(0, grp.n_tiles, 5, ws, grp.default_sub_batch())
+        grp.untile(5)
+        ps = [p.clone() for p in params]
+        tables = ApplyTables([(p, u, 0) for p, u in zip(ps, grp.updates)])
+        assert not tables.fallback
+        tables.run([1 - 0.02 * 0.1], [-0.02])
+        torch.cuda.synchronize()
+        assert all(u.dtype == udt for u in grp.updates)
+        results.append(ps)
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
