@@ -123,7 +123,8 @@ def time_ns_stage(opt, reps: int) -> float:
 
 
 def time_io_stage(opt, reps: int) -> tuple[float, float]:
-    """Average ms of gather (+normaliser) and of untile for one step."""
+    """Average ms of gather (+normaliser) and of untile for one step (for a
+    fused group, the untile that applies WD/LR to the parameters in place)."""
     s = torch.cuda.current_stream()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     torch.cuda.synchronize()
@@ -134,7 +135,7 @@ def time_io_stage(opt, reps: int) -> tuple[float, float]:
     ev[1].record(s)
     for _ in range(reps):
         for g in opt._groups:
-            g["tiles"].untile()
+            g["tiles"].untile(g["steps"], opt._lrwd)
     ev[2].record(s)
     ev[2].synchronize()
     return ev[0].elapsed_time(ev[1]) / reps, ev[1].elapsed_time(ev[2]) / reps
@@ -365,7 +366,9 @@ def main():
     n_tiles = sum(g["tiles"].n_tiles for g in opt._groups)
     traffic = NS5_STAGE_TRAFFIC_BYTES.get(args.config) if ns_path() == "stream" else None
     n_el = sum(p.numel() for p in params)
-    # bytes per element: update (untile writes it, the WD/LR pass reads it), parameter
+    # bytes per element: update (untile writes it, the WD/LR pass reads it), parameter;
+    # fused: the untile reads the NS tile and reads and writes the parameter
+    fused = all(g["tiles"].fused for g in opt._groups)
     ub = torch.empty(0, dtype=opt._groups[0]["tiles"].upd_dtype).element_size()
     pb = params[0].element_size()
     ns_tflops = flops / (ns_ms * 1e-3) / 1e12
@@ -400,10 +403,11 @@ def main():
         "gather_ms": round(gather_ms, 3),
         "gather_gbs": round(14.0 * n_el / (gather_ms * 1e-3) / 1e9, 1),
         "untile_ms": round(untile_ms, 3),
-        "untile_gbs": round((2 + ub) * n_el / (untile_ms * 1e-3) / 1e9, 1),
+        "untile_gbs": round(((2 + 2 * pb) if fused else (2 + ub)) * n_el / (untile_ms * 1e-3) / 1e9, 1),
+        "untile_applies_wd_lr": fused,
         "apply_ms": round(apply_ms, 3),
-        "apply_gbs": round((2 * pb + ub) * n_el / (apply_ms * 1e-3) / 1e9, 1),
-        "update_dtype": str(opt._groups[0]["tiles"].upd_dtype).replace("torch.", ""),
+        "apply_gbs": None if fused else round((2 * pb + ub) * n_el / (apply_ms * 1e-3) / 1e9, 1),
+        "update_dtype": None if fused else str(opt._groups[0]["tiles"].upd_dtype).replace("torch.", ""),
         "roofline": {
             "kernel": NS_KERNELS.get(ns_path(), ns_path()),
             "bound": "mfma",

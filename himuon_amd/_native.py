@@ -46,7 +46,7 @@ class ParamDesc(ctypes.Structure):
         ("upd_scale", c_float),
         ("mu", c_float),
         ("nesterov", c_int32),
-        ("reserved", c_int32),
+        ("group", c_int32),
     ]
 
 
@@ -122,6 +122,10 @@ _SIGNATURES = {
     "himuon_untile": (
         c_int,
         [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p],
+    ),
+    "himuon_untile_apply": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p],
     ),
     "himuon_apply_chunk_elems": (c_int64, []),
     "himuon_apply_updates": (
@@ -315,6 +319,19 @@ def untile(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtype, tiles)
             _stream(),
         ),
         "himuon_untile",
+    )
+
+
+def untile_apply(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, param_dtype, tiles, scale_alpha):
+    """Untile with the group's WD/LR applied in place to the parameters the
+    descriptors point at; scale_alpha: fp32 device tensor (s_g, alpha_g) per
+    group, read when the kernel runs."""
+    _check(
+        load().himuon_untile_apply(
+            desc_table.data_ptr(), n_params, n_tiles, tile_h, tile_w, mp, np_, dtype_code(param_dtype),
+            tiles.data_ptr(), scale_alpha.data_ptr(), _stream(),
+        ),
+        "himuon_untile_apply",
     )
 
 

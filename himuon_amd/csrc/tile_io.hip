@@ -229,10 +229,42 @@ __global__ __launch_bounds__(kThreads) void tile_scale_kernel(const float* __res
 // Untile, plain tiles: update[pr, pc] = scale * NS(i, j). Work item = (tile,
 // slab of `rows` NS rows); only NS columns < tile_w hold data.
 // ---------------------------------------------------------------------------
-template <int DT>
+// APPLY: the descriptor's `update` is the parameter itself (ld_upd its row
+// stride) and the weight decay and learning rate of its group are applied in
+// place instead of storing the update (himuon_untile_apply):
+//     p = rd(fma(alpha_g, rd(u), rd(p * s_g))),  u = upd_scale * NS (fp32)
+// sa holds (s_g, alpha_g) per group, in device memory.
+template <bool APPLY, int DT>
+HM_DEV void put8(const HimuonParamDesc& P, int64_t o, const float (&y)[8], bool full, int valid,
+                 const float* __restrict__ sa) {
+#pragma clang fp contract(off)
+  if constexpr (APPLY) {
+    const float s = sa[2 * P.group], alpha = sa[2 * P.group + 1];
+    if (full) {
+      float p[8];
+      load8<DT>(P.update, o, p);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p[e] = __builtin_fmaf(alpha, round_to<DT>(y[e]), round_to<DT>(p[e] * s));
+      store8<DT>(P.update, o, p);
+    } else {
+      for (int e = 0; e < valid; ++e) {
+        const float p1 = round_to<DT>(load_elem<DT>(P.update, o + e) * s);
+        store_elem<DT>(P.update, o + e, __builtin_fmaf(alpha, round_to<DT>(y[e]), p1));
+      }
+    }
+  } else {
+    if (full) {
+      store8<DT>(P.update, o, y);
+    } else {
+      for (int e = 0; e < valid; ++e) store_elem<DT>(P.update, o + e, y[e]);
+    }
+  }
+}
+
+template <bool APPLY, int DT>
 __global__ __launch_bounds__(kThreads) void untile_rows_kernel(
     const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
-    const uint16_t* __restrict__ tiles) {
+    const uint16_t* __restrict__ tiles, const float* __restrict__ sa) {
   const int rows = slab_rows(geo.mp, geo.np);
   const int slabs = geo.mp / rows;
   const int vcols = (geo.tile_w + 7) / 8;
@@ -271,23 +303,19 @@ __global__ __launch_bounds__(kThreads) void untile_rows_kernel(
           y[2 * e2 + 1] = sc * __uint_as_float(w[e2] & 0xffff0000u);
         }
         const int64_t ou = pr * P.ld_upd + pc;
-        if (j0 + 8 <= geo.tile_w && pc + 8 <= P.w && aligned16<DT>(P.update, ou)) {
-          store8<DT>(P.update, ou, y);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (j0 + e < geo.tile_w && pc + e < P.w) store_elem<DT>(P.update, ou + e, y[e]);
-        }
+        const bool full = j0 + 8 <= geo.tile_w && pc + 8 <= P.w && aligned16<DT>(P.update, ou);
+        const int valid = (int)min<int64_t>(min(8, geo.tile_w - j0), P.w - pc);
+        put8<APPLY, DT>(P, ou, y, full, valid, sa);
       }
     }
   }
 }
 
 // Untile, transposed tiles: update[pr, pc] = scale * NS(pc_local, pr_local).
-template <int DT>
+template <bool APPLY, int DT>
 __global__ __launch_bounds__(kThreads) void untile_trans_kernel(
     const HimuonParamDesc* __restrict__ params, int n_params, int64_t n_tiles, Geo geo,
-    const uint16_t* __restrict__ tiles) {
+    const uint16_t* __restrict__ tiles, const float* __restrict__ sa) {
   __shared__ uint16_t sT[kBlk * kBlkPitch];  // [tile row tr][tile col tc]
   const int bi_n = geo.mp / kBlk, bj_n = geo.np / kBlk;
   const int blocks = bi_n * bj_n;
@@ -329,13 +357,9 @@ __global__ __launch_bounds__(kThreads) void untile_trans_kernel(
       y[2 * k + 1] = sc * __uint_as_float(w[k] & 0xffff0000u);
     }
     const int64_t ou = pr * P.ld_upd + pc;
-    if (tc + 8 <= geo.tile_w && pc + 8 <= P.w && aligned16<DT>(P.update, ou)) {
-      store8<DT>(P.update, ou, y);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (tc + e < geo.tile_w && pc + e < P.w) store_elem<DT>(P.update, ou + e, y[e]);
-    }
+    const bool full = tc + 8 <= geo.tile_w && pc + 8 <= P.w && aligned16<DT>(P.update, ou);
+    const int valid = (int)min<int64_t>(min(8, geo.tile_w - tc), P.w - pc);
+    put8<APPLY, DT>(P, ou, y, full, valid, sa);
   }
 }
 
@@ -406,11 +430,11 @@ extern "C" int himuon_tile_scale(const float* partials, int partials_per_tile, i
   return (int)hipGetLastError();
 }
 
-extern "C" int himuon_untile(const HimuonParamDesc* params_dev, int n_params, int64_t n_tiles,
-                             int tile_h, int tile_w, int mp, int np, int dtype,
-                             const uint16_t* tiles_bf16, void* stream) {
-  if (!geo_ok(tile_h, tile_w, mp, np) || n_params <= 0 || n_tiles < 0 || !params_dev ||
-      !tiles_bf16)
+namespace {
+template <bool APPLY>
+int untile_launch(const HimuonParamDesc* params_dev, int n_params, int64_t n_tiles, int tile_h, int tile_w,
+                  int mp, int np, int dtype, const uint16_t* tiles_bf16, const float* sa, void* stream) {
+  if (!geo_ok(tile_h, tile_w, mp, np) || n_params <= 0 || n_tiles < 0 || !params_dev || !tiles_bf16)
     return HIMUON_EINVAL;
   if (n_tiles == 0) return 0;
   const Geo geo{tile_h, tile_w, mp, np};
@@ -419,19 +443,36 @@ extern "C" int himuon_untile(const HimuonParamDesc* params_dev, int n_params, in
   if (tile_h > tile_w) {
     const dim3 grid((unsigned)xcd_grid(n_tiles * (mp / kBlk) * (np / kBlk)));
     switch (dtype) {
-      case HIMUON_DTYPE_F32: hipLaunchKernelGGL(untile_trans_kernel<HIMUON_DTYPE_F32>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
-      case HIMUON_DTYPE_BF16: hipLaunchKernelGGL(untile_trans_kernel<HIMUON_DTYPE_BF16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
-      case HIMUON_DTYPE_F16: hipLaunchKernelGGL(untile_trans_kernel<HIMUON_DTYPE_F16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
+      case HIMUON_DTYPE_F32: hipLaunchKernelGGL((untile_trans_kernel<APPLY, HIMUON_DTYPE_F32>), grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, sa); break;
+      case HIMUON_DTYPE_BF16: hipLaunchKernelGGL((untile_trans_kernel<APPLY, HIMUON_DTYPE_BF16>), grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, sa); break;
+      case HIMUON_DTYPE_F16: hipLaunchKernelGGL((untile_trans_kernel<APPLY, HIMUON_DTYPE_F16>), grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, sa); break;
       default: return HIMUON_EINVAL;
     }
   } else {
     const dim3 grid((unsigned)std::min<int64_t>(n_tiles * (mp / slab_rows(mp, np)), (int64_t)4 * num_cus()));
     switch (dtype) {
-      case HIMUON_DTYPE_F32: hipLaunchKernelGGL(untile_rows_kernel<HIMUON_DTYPE_F32>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
-      case HIMUON_DTYPE_BF16: hipLaunchKernelGGL(untile_rows_kernel<HIMUON_DTYPE_BF16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
-      case HIMUON_DTYPE_F16: hipLaunchKernelGGL(untile_rows_kernel<HIMUON_DTYPE_F16>, grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16); break;
+      case HIMUON_DTYPE_F32: hipLaunchKernelGGL((untile_rows_kernel<APPLY, HIMUON_DTYPE_F32>), grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, sa); break;
+      case HIMUON_DTYPE_BF16: hipLaunchKernelGGL((untile_rows_kernel<APPLY, HIMUON_DTYPE_BF16>), grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, sa); break;
+      case HIMUON_DTYPE_F16: hipLaunchKernelGGL((untile_rows_kernel<APPLY, HIMUON_DTYPE_F16>), grid, block, 0, s, params_dev, n_params, n_tiles, geo, tiles_bf16, sa); break;
       default: return HIMUON_EINVAL;
     }
   }
   return (int)hipGetLastError();
+}
+}  // namespace
+
+extern "C" int himuon_untile(const HimuonParamDesc* params_dev, int n_params, int64_t n_tiles,
+                             int tile_h, int tile_w, int mp, int np, int dtype,
+                             const uint16_t* tiles_bf16, void* stream) {
+  return untile_launch<false>(params_dev, n_params, n_tiles, tile_h, tile_w, mp, np, dtype, tiles_bf16,
+                              nullptr, stream);
+}
+
+extern "C" int himuon_untile_apply(const HimuonParamDesc* params_dev, int n_params, int64_t n_tiles,
+                                   int tile_h, int tile_w, int mp, int np, int param_dtype,
+                                   const uint16_t* tiles_bf16, const float* scale_alpha_dev,
+                                   void* stream) {
+  if (!scale_alpha_dev) return HIMUON_EINVAL;
+  return untile_launch<true>(params_dev, n_params, n_tiles, tile_h, tile_w, mp, np, param_dtype, tiles_bf16,
+                             scale_alpha_dev, stream);
 }

@@ -49,6 +49,7 @@ class TileGroup:
         device: torch.device,
         dtype: torch.dtype,
         upd_dtype: torch.dtype | None = None,
+        apply_groups: list[int] | None = None,
     ):
         self.tile_h, self.tile_w = int(tile_h), int(tile_w)
         self.m, self.n, self.mp, self.np, self.trans = nat.ns_geometry(self.tile_h, self.tile_w)
@@ -58,6 +59,18 @@ class TileGroup:
         # when the only consumer of the update rounds it to that dtype first.
         self.upd_dtype = dtype if upd_dtype is None else upd_dtype
         self.params = params
+        # Fused mode (apply_groups given): the untile applies each parameter's
+        # group WD/LR to the parameter in place (himuon_untile_apply) and no
+        # update tensors exist.
+        self.fused = apply_groups is not None
+        if self.fused:
+            pdts = {p.dtype for p in params}
+            if len(pdts) != 1:
+                raise TypeError(f"fused untile needs one parameter dtype per group, got {pdts}")
+            self.upd_dtype = next(iter(pdts))
+            for p in params:
+                self._check_tensor(p.data, "parameter")
+        self.apply_groups = list(apply_groups) if self.fused else None
         counts = []
         for g in grads:
             h, w = g.shape
@@ -72,7 +85,7 @@ class TileGroup:
         self.alt = torch.empty(shape, device=device, dtype=torch.bfloat16)
         self.partials = torch.empty((self.n_tiles, self.ppt), device=device, dtype=torch.float32)
         self.inv = torch.empty((self.n_tiles,), device=device, dtype=torch.float32)
-        self.updates = [torch.empty(g.shape, device=device, dtype=self.upd_dtype) for g in grads]
+        self.updates = [] if self.fused else [torch.empty(g.shape, device=device, dtype=self.upd_dtype) for g in grads]
         self.upd_scales = list(upd_scales)
         self._sig = None
         self.desc = None
@@ -102,7 +115,7 @@ class TileGroup:
                 raise TypeError(f"bucket dtype {self.dtype} but grad dtype {g.dtype}")
             if m is not None:
                 self._check_tensor(m, "momentum buffer")
-            u = self.updates[i]
+            u = self.params[i].data if self.fused else self.updates[i]
             h, w = g.shape
             d = nat.ParamDesc()
             d.grad = g.data_ptr()
@@ -118,6 +131,7 @@ class TileGroup:
             d.upd_scale = self.upd_scales[i]
             d.mu = float(mus[i])
             d.nesterov = 1 if nesterovs[i] else 0
+            d.group = self.apply_groups[i] if self.fused else 0
             descs.append(d)
         self.desc = nat.make_desc_table(descs, self.device)
         self._sig = sig
@@ -126,7 +140,7 @@ class TileGroup:
     # -- launches ----------------------------------------------------------
     def gather(self) -> None:
         nat.momentum_gather(
-            self.desc, len(self.updates), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
+            self.desc, len(self.tile0), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
             self.dtype, self.tiles, self.partials,
         )
         nat.tile_scale(self.partials, self.ppt, self.n_tiles, self.inv)
@@ -149,9 +163,19 @@ class TileGroup:
         """Buffer holding the NS output after `steps` iterations."""
         return self.tiles if steps % 2 == 0 else self.alt
 
-    def untile(self, steps: int = 5) -> None:
+    def untile(self, steps: int = 5, scale_alpha: torch.Tensor | None = None) -> None:
+        """Write the update tensors, or, in fused mode, apply the WD/LR of
+        scale_alpha (device (s_g, alpha_g) per group) to the parameters."""
+        if self.fused:
+            if scale_alpha is None:
+                raise ValueError("fused TileGroup.untile needs the (scale, alpha) device table")
+            nat.untile_apply(
+                self.desc, len(self.tile0), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
+                self.upd_dtype, self.result(steps), scale_alpha,
+            )
+            return
         nat.untile(
-            self.desc, len(self.updates), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
+            self.desc, len(self.tile0), self.n_tiles, self.tile_h, self.tile_w, self.mp, self.np,
             self.upd_dtype, self.result(steps),
         )
 

@@ -57,6 +57,11 @@ class HiMuon(Optimizer):
             eager steps (the name is kept for drop-in compatibility).
     """
 
+    # Muon buckets apply their WD/LR inside the untile (himuon_untile_apply)
+    # when their parameters allow it; False keeps update tensors and the
+    # separate WD/LR pass for every bucket (same parameters, bit for bit).
+    _fuse_untile: bool = True
+
     def __init__(
         self,
         params,
@@ -105,6 +110,9 @@ class HiMuon(Optimizer):
         self._apply_tables: "ApplyTables | None" = None  # device tables for _pending_updates
         # Fused AdamW fallback: persistent update buffers and device tables,
         # rebuilt when the set of (param, grad storage) changes.
+        # Device (scale, alpha) per param group, written before each step and
+        # read by the fused untile+WD/LR kernel (also during graph replay).
+        self._lrwd: "torch.Tensor | None" = None
         self._adamw_updates: dict = {}
         self._adamw_tables: "AdamwTables | None" = None
         self._adamw_sig: "tuple | None" = None
@@ -161,14 +169,37 @@ class HiMuon(Optimizer):
         self._adamw_tables = None
         self._adamw_sig = None
 
+    def _scale_alpha(self) -> list[float]:
+        """(1 - lr*wd, -lr) per param group: the two factors of p.mul_(1 - lr*wd);
+        p.add_(u, alpha=-lr) (himuon.py:222-228, 345-348); 1.0 when wd == 0."""
+        out = []
+        for group in self.param_groups:
+            lr, weight_decay = group["lr"], group["weight_decay"]
+            out += [1 - lr * weight_decay if weight_decay > 0.0 else 1.0, -lr]
+        return out
+
+    def _write_lrwd(self, device) -> None:
+        """Current (scale, alpha) of every group into the device table the fused
+        untile reads; stream-ordered before the step body or graph replay."""
+        vals = self._scale_alpha()
+        n = max(len(vals), 2 * nat.APPLY_MAX_GROUPS)
+        if self._lrwd is None or self._lrwd.device != device:
+            self._lrwd = torch.zeros(n, device=device, dtype=torch.float32)
+        self._lrwd[: len(vals)].copy_(torch.tensor(vals, dtype=torch.float32))
+
     def _apply_pending_updates(self):
         """WD + LR application after replay, reading the current group lr/wd:
         one multi-tensor HIP launch per dtype pair (himuon_apply_updates) with
-        lr/wd passed as host scalars, so schedules need no recapture."""
+        lr/wd passed as host scalars, so schedules need no recapture. Entries
+        without an update tensor belong to fused groups, whose WD/LR the untile
+        already applied inside the graph."""
         if not self._pending_updates:
             return
         if self._apply_tables is None:
-            self._apply_tables = ApplyTables(self._pending_updates)
+            todo = [e for e in self._pending_updates if e[1] is not None]
+            if not todo:
+                return
+            self._apply_tables = ApplyTables(todo)
         scales, alphas = [], []
         for group in self.param_groups:
             lr, weight_decay = group["lr"], group["weight_decay"]
@@ -426,6 +457,18 @@ class HiMuon(Optimizer):
 
     def _build_groups(self, plan: list[dict]) -> list[dict]:
         group_to_idx = {id(g): i for i, g in enumerate(self.param_groups)}
+
+        def fusable(params, gidx) -> bool:
+            # The untile applies WD/LR in place: one parameter dtype the kernels
+            # take, row-major 2-D parameters, group indices inside the table.
+            pd = {p.dtype for p in params}
+            return (
+                self._fuse_untile
+                and len(pd) == 1 and next(iter(pd)) in nat.DTYPE_CODES
+                and all(p.is_cuda and p.ndim == 2 and (p.stride(1) == 1 or p.shape[1] == 1) for p in params)
+                and max(gidx) < nat.APPLY_MAX_GROUPS
+            )
+
         out = []
         for bucket in plan:
             tile_h, tile_w, _f, dtype = bucket["bucket_key"]
@@ -433,6 +476,7 @@ class HiMuon(Optimizer):
             steps = {e[1]["ns_steps"] for e in entries}
             assert len(steps) <= 1, f"cross-layer NS requires a uniform ns_steps per bucket; saw {steps}"
             params = [e[0] for e in entries]
+            gidx = [group_to_idx[id(e[1])] for e in entries]
             grp = TileGroup(
                 params=params,
                 grads=[p.grad for p in params],
@@ -445,6 +489,7 @@ class HiMuon(Optimizer):
                 device=params[0].grad.device,
                 dtype=dtype,
                 upd_dtype=update_dtype(params, dtype),
+                apply_groups=gidx if fusable(params, gidx) else None,
             )
             self._concat_buffers[bucket["bucket_key"]] = grp.tiles
             out.append(
@@ -461,6 +506,7 @@ class HiMuon(Optimizer):
             (h, w), dtype, steps = fg["key"]
             entries = fg["entries"]
             params = [p for p, _ in entries]
+            gidx = [group_to_idx[id(g)] for _, g in entries]
             # One tile per matrix: tile = (h, w); lr scale from p.shape (himuon.py:872-874).
             grp = TileGroup(
                 params=params,
@@ -474,6 +520,7 @@ class HiMuon(Optimizer):
                 device=params[0].grad.device,
                 dtype=dtype,
                 upd_dtype=update_dtype(params, dtype),
+                apply_groups=gidx if fusable(params, gidx) else None,
             )
             out.append(
                 {
@@ -546,9 +593,18 @@ class HiMuon(Optimizer):
                 ns_launches += 1
                 total_B += c
                 ofs += c
-            grp.untile(g["steps"])
-            for (p, grp_dict), gi, upd in zip(g["entries"], g["group_idx"], grp.updates):
-                self._apply_wd_and_update(p, upd, grp_dict["weight_decay"], grp_dict["lr"], gi)
+            if grp.fused:
+                # WD/LR applied by the untile itself, from the (scale, alpha)
+                # table written before this step; the graph path still lists
+                # the parameters as pending (without an update tensor).
+                grp.untile(g["steps"], self._lrwd)
+                if self._in_graph_region:
+                    for (p, _), gi in zip(g["entries"], g["group_idx"]):
+                        self._pending_updates.append((p, None, gi))
+            else:
+                grp.untile(g["steps"])
+                for (p, grp_dict), gi, upd in zip(g["entries"], g["group_idx"], grp.updates):
+                    self._apply_wd_and_update(p, upd, grp_dict["weight_decay"], grp_dict["lr"], gi)
         ns_ms = 0.0
         if use_events and ev_pairs:
             ev_pairs[-1][1].synchronize()
@@ -605,6 +661,9 @@ class HiMuon(Optimizer):
         if closure is not None:
             loss = closure()
         self._check_device()
+        dev = next((p.grad.device for g in self.param_groups for p in g["params"] if p.grad is not None), None)
+        if dev is not None and dev.type == "cuda":
+            self._write_lrwd(dev)
         if not self._cuda_graph_enabled or not torch.cuda.is_available():
             self._step_body()
             return loss

@@ -70,7 +70,7 @@ typedef struct HimuonParamDesc {
   float upd_scale;    /* update = upd_scale * NS output (lr adjustment)          */
   float mu;           /* momentum coefficient                                    */
   int32_t nesterov;   /* nonzero: Nesterov momentum                              */
-  int32_t reserved;
+  int32_t group;      /* param group index (read by himuon_untile_apply only)    */
 } HimuonParamDesc;
 
 /* Library ABI version (HIMUON_ABI_VERSION it was built with). */
@@ -157,6 +157,25 @@ int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles,
 int himuon_untile(const HimuonParamDesc* params_dev, int n_params,
                   int64_t n_tiles, int tile_h, int tile_w, int mp, int np,
                   int dtype, const uint16_t* tiles_bf16, void* stream);
+
+/*
+ * Untile and apply in place: like himuon_untile, but each descriptor's
+ * `update` is the parameter itself (ld_upd its row stride, param_dtype its
+ * dtype) and, instead of storing the update, the weight decay and learning
+ * rate of the parameter's group (descriptor field `group`) are applied:
+ *     u = upd_scale * float(NS tile value)                      (fp32)
+ *     p = rd(fma(alpha[g], rd(u), rd(float(p) * scale[g])))      rd = round to param_dtype
+ * with scale[g] = scale_alpha_dev[2 g], alpha[g] = scale_alpha_dev[2 g + 1]
+ * read from DEVICE memory when the kernel runs, so a captured graph picks up
+ * learning-rate and weight-decay changes written there before each replay.
+ * The parameters end exactly as himuon_untile followed by
+ * himuon_apply_updates would leave them. Replaces the untile plus the
+ * outside-graph WD/LR of the Muon parameters (himuon.py:315-348, 215-228).
+ */
+int himuon_untile_apply(const HimuonParamDesc* params_dev, int n_params,
+                        int64_t n_tiles, int tile_h, int tile_w, int mp, int np,
+                        int param_dtype, const uint16_t* tiles_bf16,
+                        const float* scale_alpha_dev, void* stream);
 
 /*
  * Weight decay + learning-rate application, outside the captured graph

@@ -96,23 +96,64 @@ def test_step_matches_oracle(name, shapes, tile, dtype):
 
 
 def test_update_tensor_matches_oracle_per_tile():
-    """One step; the update tensor of each param vs the oracle's, per tile
-    (relative Frobenius), bit-exact momentum."""
+    """The update tensor (non-fused untile) of one param vs the oracle's, per
+    tile (relative Frobenius), bit-exact momentum."""
+    from himuon_amd.engine import TileGroup
+
     shapes, T = [(1024, 1536)], 512
     model = make_model(shapes, torch.float32)
-    opt = HiMuon(muon_groups(model), tile_size=T, cuda_graph=True, cuda_graph_warmup=0)
     seed_grads(model, 7)
-    g = _np(model[0].weight.grad)
-    opt.step()  # capture + replay
-    upd = [u for (_, u, _) in opt._pending_updates][0]
-    ge, _ = O.momentum(g, np.zeros_like(g), 0.95, True)
+    p = model[0].weight
+    g = _np(p.grad)
+    mom = torch.zeros_like(p.grad)
+    grp = TileGroup(params=[p], grads=[p.grad], moms=[mom], tile_h=T, tile_w=T,
+                    upd_scales=[float(O.lr_scale((T, T)))], mus=[0.95], nesterovs=[True],
+                    device=p.device, dtype=torch.float32)
+    ws = torch.empty(grp.workspace_bytes(grp.default_sub_batch()), device=DEV, dtype=torch.uint8)
+    grp.gather()
+    grp.ns(0, grp.n_tiles, 5, ws, grp.default_sub_batch())
+    grp.untile(5)
+    ge, nb = O.momentum(g, np.zeros_like(g), 0.95, True)
+    assert np.array_equal(_np(mom), nb)
     ref = O.untile(O.ns5_staged(O.tile(ge, T, T)), *shapes[0]) * np.float32(O.lr_scale((T, T)))
-    got = _np(upd)
+    got = _np(grp.updates[0])
     for r in range(2):
         for c in range(3):
             sl = (slice(r * T, (r + 1) * T), slice(c * T, (c + 1) * T))
             e = np.linalg.norm(got[sl] - ref[sl]) / np.linalg.norm(ref[sl])
             assert e < 2e-2, (r, c, e)
+
+
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("cuda_graph", [False, True])
+def test_fused_untile_apply_matches_unfused(pdt, cuda_graph):
+    """The fused untile (WD/LR applied in place, inside the graph) leaves the
+    parameters bit-identical to the unfused path (update tensors, then the
+    WD/LR pass), over several steps with an lr/wd change between steps, which
+    the fused path reads from its device table without a recapture."""
+    shapes = [(512, 1024), (256, 512), (700, 300)]
+    m_f = make_model(shapes, pdt)
+    m_u = copy.deepcopy(m_f)
+    kw = dict(lr=0.02, weight_decay=0.05, tile_size=256, cuda_graph=cuda_graph, cuda_graph_warmup=2)
+    o_f = HiMuon(muon_groups(m_f, wd=0.05), **kw)
+    o_u = HiMuon(muon_groups(m_u, wd=0.05), **kw)
+    o_u._fuse_untile = False
+    for k in range(7):
+        if k == 5:
+            for o in (o_f, o_u):
+                o.param_groups[0]["lr"] = 0.01
+                o.param_groups[0]["weight_decay"] = 0.1
+        seed_grads(m_f, 400 + k)
+        seed_grads(m_u, 400 + k)
+        o_f.step()
+        o_u.step()
+    assert all(g["tiles"].fused for g in o_f._groups)
+    assert not any(g["tiles"].fused for g in o_u._groups)
+    if cuda_graph:
+        assert o_f._cuda_graph is not None and o_f._pending_updates
+        assert all(u is None for _, u, _ in o_f._pending_updates)
+    for a, b in zip(m_f.parameters(), m_u.parameters()):
+        assert torch.equal(a, b)
 
 
 # ---------------------------------------------------------------------------
