@@ -51,10 +51,10 @@ PEAK_HBM_GBS = 8000.0
 # HBM bytes the NS5 stage moves per step, measured with rocprofv3 --pmc
 # FETCH_SIZE and WRITE_SIZE on this config, each scaled by what the counter
 # reads for this script's 256 MiB device copy (FETCH_SIZE x 1.9995, WRITE_SIZE
-# x 1.0): per 3,465-tile dispatch GramA reads 1.865 GB, GramB 2.769 GB, Apply
-# 4.827 GB, the X0 scaling 1.816 GB, each writing 1.817 GB; 20 + 20 + 20 + 4
+# x 1.0): per 3,465-tile dispatch GramA reads 1.837 GB, GramB 2.738 GB, Apply
+# 4.968 GB, the X0 scaling 1.816 GB, each writing 1.817 GB; 20 + 20 + 20 + 4
 # dispatches per step. Other configs: not measured (null).
-NS5_STAGE_TRAFFIC_BYTES = {"qwen3-4b": 312.75e9}
+NS5_STAGE_TRAFFIC_BYTES = {"qwen3-4b": 314.44e9}
 
 CONFIGS = {
     # name: (layers, [(h, w) per layer], tile_size, param dtype, description)

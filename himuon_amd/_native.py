@@ -127,6 +127,9 @@ _SIGNATURES = {
         c_int,
         [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p],
     ),
+    "himuon_write_scale_alpha": (
+        c_int, [c_void_p, ctypes.POINTER(c_float), ctypes.POINTER(c_float), c_int, c_void_p],
+    ),
     "himuon_apply_chunk_elems": (c_int64, []),
     "himuon_apply_updates": (
         c_int,
@@ -333,6 +336,19 @@ def untile_apply(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, param_d
         ),
         "himuon_untile_apply",
     )
+
+
+def write_scale_alpha(table, scales, alphas):
+    """(s_g, alpha_g) per group into the fp32 device table the fused untile
+    reads, as a kernel on the current stream (no host synchronisation)."""
+    n = len(scales)
+    if n != len(alphas) or not 0 < n <= APPLY_MAX_GROUPS or table.numel() < 2 * n:
+        raise ValueError(f"write_scale_alpha: {n} groups for a table of {table.numel()} floats")
+    if table.dtype != torch.float32 or not table.is_cuda:
+        raise TypeError("write_scale_alpha: table must be an fp32 device tensor")
+    cs = (c_float * n)(*scales)
+    ca = (c_float * n)(*alphas)
+    _check(load().himuon_write_scale_alpha(table.data_ptr(), cs, ca, n, _stream()), "himuon_write_scale_alpha")
 
 
 def lr_scale(block_shape, lr_adjust: str = "tile") -> float:

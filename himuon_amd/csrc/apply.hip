@@ -30,6 +30,19 @@ struct ApplyScalars {
   float alpha[HIMUON_APPLY_MAX_GROUPS];
 };
 
+// (s_g, alpha_g) pairs into the device table the fused untile reads. The
+// values travel as launch arguments, so the write is stream-ordered behind
+// earlier work (a graph replay still reading the table) and needs no host
+// buffer that outlives the call.
+__global__ __launch_bounds__(64) void write_scale_alpha_kernel(float* __restrict__ out, ApplyScalars sc,
+                                                               int n_groups) {
+  const int g = threadIdx.x;
+  if (g < n_groups) {
+    out[2 * g] = sc.s[g];
+    out[2 * g + 1] = sc.alpha[g];
+  }
+}
+
 // Descriptor owning chunk q: the last d with descs[d].chunk0 <= q.
 HM_DEV int find_desc(const HimuonApplyDesc* __restrict__ d, int n, int64_t q) {
   int lo = 0, hi = n - 1;
@@ -96,6 +109,22 @@ int launch_pd(int ud, const HimuonApplyDesc* d, int n, int64_t n_chunks, const A
 }  // namespace
 
 extern "C" int64_t himuon_apply_chunk_elems(void) { return kChunk; }
+
+extern "C" int himuon_write_scale_alpha(float* scale_alpha_dev, const float* scale_by_group,
+                                        const float* alpha_by_group, int n_groups, void* stream) {
+  if (!scale_alpha_dev || !scale_by_group || !alpha_by_group || n_groups <= 0 ||
+      n_groups > HIMUON_APPLY_MAX_GROUPS)
+    return HIMUON_EINVAL;
+  ApplyScalars sc{};
+  for (int g = 0; g < n_groups; ++g) {
+    sc.s[g] = scale_by_group[g];
+    sc.alpha[g] = alpha_by_group[g];
+  }
+  static_assert(HIMUON_APPLY_MAX_GROUPS <= 64, "one thread per group");
+  hipLaunchKernelGGL(write_scale_alpha_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     scale_alpha_dev, sc, n_groups);
+  return (int)hipGetLastError();
+}
 
 extern "C" int himuon_apply_updates(const HimuonApplyDesc* descs_dev, int n_descs, int64_t n_chunks,
                                     int param_dtype, int update_dtype, const float* scale_by_group,

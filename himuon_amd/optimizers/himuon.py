@@ -180,12 +180,15 @@ class HiMuon(Optimizer):
 
     def _write_lrwd(self, device) -> None:
         """Current (scale, alpha) of every group into the device table the fused
-        untile reads; stream-ordered before the step body or graph replay."""
-        vals = self._scale_alpha()
-        n = max(len(vals), 2 * nat.APPLY_MAX_GROUPS)
+        untile reads: one small kernel on the current stream, ordered after the
+        previous replay (which may still read the table) and before this step's
+        body or replay, without a host synchronisation. Groups beyond what the
+        table holds are never fused (their buckets take the outside-graph
+        WD/LR), so only the first APPLY_MAX_GROUPS are written."""
+        vals = self._scale_alpha()[: 2 * nat.APPLY_MAX_GROUPS]
         if self._lrwd is None or self._lrwd.device != device:
-            self._lrwd = torch.zeros(n, device=device, dtype=torch.float32)
-        self._lrwd[: len(vals)].copy_(torch.tensor(vals, dtype=torch.float32))
+            self._lrwd = torch.zeros(2 * nat.APPLY_MAX_GROUPS, device=device, dtype=torch.float32)
+        nat.write_scale_alpha(self._lrwd, vals[0::2], vals[1::2])
 
     def _apply_pending_updates(self):
         """WD + LR application after replay, reading the current group lr/wd:
@@ -638,7 +641,9 @@ class HiMuon(Optimizer):
                     )
 
     def _capture_graph(self) -> None:
-        """Capture momentum..untile into a hipGraph; WD/LR stay outside."""
+        """Capture momentum..untile into a hipGraph. The fused untile reads WD/LR
+        from the device table step() rewrites before each replay; the
+        remaining updates get theirs after replay."""
         self._ensure_device_state()  # allocate everything before capture
         self._prepare_adamw()
         torch.cuda.synchronize()

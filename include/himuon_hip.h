@@ -178,6 +178,19 @@ int himuon_untile_apply(const HimuonParamDesc* params_dev, int n_params,
                         const float* scale_alpha_dev, void* stream);
 
 /*
+ * Write the table himuon_untile_apply reads: scale_alpha_dev[2 g] =
+ * scale_by_group[g], scale_alpha_dev[2 g + 1] = alpha_by_group[g] for
+ * g < n_groups (at most HIMUON_APPLY_MAX_GROUPS). scale_by_group and
+ * alpha_by_group are HOST arrays, copied into the launch arguments, so the
+ * write is a kernel on `stream`: ordered after earlier work on it (a graph
+ * replay that still reads the table) and asynchronous to the host, like the
+ * Python-float lr and wd the reference's outside-graph WD/LR uses
+ * (himuon.py:215-228). Call it outside any captured graph, before each replay.
+ */
+int himuon_write_scale_alpha(float* scale_alpha_dev, const float* scale_by_group,
+                             const float* alpha_by_group, int n_groups, void* stream);
+
+/*
  * Weight decay + learning-rate application, outside the captured graph
  * (replaces _apply_pending_updates, himuon.py:215-228, and the eager
  * _apply_wd_and_update, himuon.py:333-348). One descriptor per parameter, in

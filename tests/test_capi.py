@@ -80,6 +80,20 @@ def test_adamw_argument_errors(lib):
     assert lib.himuon_adamw_step(8, 1, 4, 0, z, one, one, 1, 8, z) == -22
 
 
+def test_scale_alpha_argument_errors(lib):
+    z = None
+    one = (ctypes.c_float * 1)(1.0)
+    many = (ctypes.c_float * 40)(*([1.0] * 40))
+    # null table or host arrays, no groups, more groups than the table holds
+    assert lib.himuon_write_scale_alpha(z, one, one, 1, z) == -22
+    assert lib.himuon_write_scale_alpha(8, z, one, 1, z) == -22
+    assert lib.himuon_write_scale_alpha(8, one, z, 1, z) == -22
+    assert lib.himuon_write_scale_alpha(8, one, one, 0, z) == -22
+    assert lib.himuon_write_scale_alpha(8, many, many, 33, z) == -22
+    # the fused untile needs its (scale, alpha) table
+    assert lib.himuon_untile_apply(8, 1, 4, 512, 512, 512, 512, 1, 8, z, z) == -22
+
+
 def test_partials_per_tile(lib):
     assert lib.himuon_gather_partials_per_tile(512, 512, 512, 512) == 512 // 32  # 32-row slabs
     assert lib.himuon_gather_partials_per_tile(256, 1024, 256, 1024) == 256 // 32

@@ -146,3 +146,23 @@ def test_narrow_update_storage_gives_identical_params(pdt):
         results.append(ps)
     for a, b in zip(*results):
         assert torch.equal(a, b)
+
+
+def test_write_scale_alpha_table():
+    """himuon_write_scale_alpha stores (s_g, alpha_g) as fp32, pairwise, and
+    leaves the entries past n_groups as they were; two writes queued on the
+    stream land in order."""
+    from himuon_amd import _native as nat
+
+    table = torch.full((2 * nat.APPLY_MAX_GROUPS,), -7.0, device=DEV)
+    scales = [1 - 0.02 * 0.1, 1.0, 0.3333333333]
+    alphas = [-0.02, -1e-3, -0.1]
+    nat.write_scale_alpha(table, [9.0, 9.0, 9.0], [9.0, 9.0, 9.0])
+    nat.write_scale_alpha(table, scales, alphas)
+    got = table.cpu().numpy()
+    want = np.full(2 * nat.APPLY_MAX_GROUPS, -7.0, dtype=np.float32)
+    want[0:6:2] = np.float32(scales)
+    want[1:6:2] = np.float32(alphas)
+    assert np.array_equal(got.view(np.int32), want.view(np.int32))
+    with pytest.raises(ValueError):
+        nat.write_scale_alpha(table, [1.0] * 33, [1.0] * 33)
