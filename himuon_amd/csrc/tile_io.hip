@@ -7,8 +7,8 @@
 // All are HBM-bound: each element is read/written once (14 B/el for fp32
 // gather, 6 B/el for fp32 untile), with 16-byte accesses on both sides.
 // Plain tiles (tile_h <= tile_w) move whole NS rows: a work item is a slab of
-// 16384 / np rows of one tile (whole tiles up to 128 x 128), walked by a
-// persistent grid, and each thread issues
+// 32, 64 or 128 NS rows of one tile (16384 elements up to np = 512, whole
+// tiles up to 128 x 128), walked by a persistent grid, and each thread issues
 // the loads of kVec 8-element vectors before using any of them, so enough
 // bytes are in flight to cover the memory latency. Tall tiles are transposed
 // through LDS in 64 x 64 blocks.
@@ -26,12 +26,15 @@ struct Geo {
   int tile_h, tile_w, mp, np;
 };
 
-// NS rows per plain-tile work item: kSlabElems / np (whole tiles at np = 128),
-// at least 32 and at most mp; mp and np are multiples of 128, so it divides mp.
+// NS rows per plain-tile work item: the largest power of two r with
+// r * np <= kSlabElems (whole tiles at np = 128), at least 32 and at most mp.
+// A power of two no larger than 128 divides mp (a multiple of 128), so the
+// slabs cover every row of the padded tile, padding rows included (np = 384
+// would give 16384 / 384 = 42 rows otherwise, which leaves rows unwritten).
 HM_HD int slab_rows(int mp, int np) {
-  int r = kSlabElems / np;
-  r = r < 32 ? 32 : r;
-  return r > mp ? mp : r;
+  int r = 32;
+  while (2 * r * np <= kSlabElems && 2 * r <= mp) r *= 2;
+  return r;
 }
 
 // Momentum for one element (himuon.py:354-356); returns the NS input and

@@ -99,9 +99,10 @@ int himuon_gather_partials_per_tile(int tile_h, int tile_w, int mp, int np);
  * nothing is written back. bf16(e) is stored at its NS tile position in
  * tiles_bf16 (n_tiles, mp, np); padding is written as zero. partials[t * P +
  * q] receives the fp32 sum of squares of the bf16 values of the q-th part of
- * NS tile t, P = himuon_gather_partials_per_tile(...): slabs of
- * max(32, min(mp, 16384 / np)) NS rows when tile_h <= tile_w, 64x64 blocks
- * (P = mp/64 * np/64) for tall tiles.
+ * NS tile t, P = himuon_gather_partials_per_tile(...): slabs of r NS rows
+ * when tile_h <= tile_w, r the largest power of two with r * np <= 16384,
+ * clamped to [32, mp] (P = mp / r); 64x64 blocks (P = mp/64 * np/64) for
+ * tall tiles.
  */
 int himuon_momentum_gather(const HimuonParamDesc* params_dev, int n_params,
                            int64_t n_tiles, int tile_h, int tile_w, int mp,

@@ -102,6 +102,22 @@ def test_partials_per_tile(lib):
     assert lib.himuon_gather_partials_per_tile(1024, 512, 512, 1024) == (512 // 64) * (1024 // 64)  # tall: 64x64 blocks
     assert lib.himuon_gather_partials_per_tile(512, 512, 500, 512) == -22  # not aligned
     assert lib.himuon_gather_partials_per_tile(512, 512, 384, 512) == -22  # mp < m
+    # np = 384: 32-row slabs (16384 / 384 = 42 rows would not divide mp = 128)
+    assert lib.himuon_gather_partials_per_tile(100, 300, 128, 384) == 4
+
+
+def test_plain_slabs_cover_every_padded_row(lib):
+    # Plain-tile gather work items are slabs of mp / P rows; they must tile the
+    # whole padded height (padding rows are written as zero by the gather), so
+    # the row count divides mp for every NS geometry, and a slab holds at most
+    # 16384 elements unless 32 rows already exceed that.
+    for mp in range(128, 2049, 128):
+        for np_ in range(mp, 4097, 128):
+            p = lib.himuon_gather_partials_per_tile(mp, np_, mp, np_)
+            assert p > 0 and mp % p == 0, (mp, np_, p)
+            rows = mp // p
+            assert rows in (32, 64, 128) and rows <= mp, (mp, np_, rows)
+            assert rows * np_ <= 16384 or rows == 32, (mp, np_, rows)
 
 
 def test_workspace_bytes(lib):

@@ -63,6 +63,9 @@ GATHER_CASES = [
     ("odd_small", [(7, 50), (50, 7)], 16, 16, "float32", True),
     ("nt_512_mixed", [(1024, 1536), (700, 300)], 512, 512, "float32", True),
     ("nt_tall_tiles", [(1024, 512)], 512, 256, "bfloat16", True),
+    # np = 384 (padded rows 100..127 are written by the last 32-row slab)
+    ("full_wide_384", [(100, 300)], 100, 300, "float32", True),
+    ("wide_384_bf16", [(256, 700)], 128, 300, "bfloat16", True),
 ]
 
 
@@ -95,6 +98,7 @@ def test_gather_bit_exact(name, shapes, th, tw, dtype, nesterov):
     grp, grads, moms = _make_group(shapes, th, tw, dtype, nesterov, seed=10, mus=mus)
     g_np = [g.float().cpu().numpy() for g in grads]
     m_np = [m.float().cpu().numpy() for m in moms]
+    grp.tiles.fill_(float("nan"))  # every element, padding included, must be written
     grp.gather()
     torch.cuda.synchronize()
     tiles = grp.tiles.float().cpu().numpy()

@@ -126,34 +126,54 @@ def test_update_tensor_matches_oracle_per_tile():
 
 @pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("cuda_graph", [False, True])
-def test_fused_untile_apply_matches_unfused(pdt, cuda_graph):
+@pytest.mark.parametrize("tile", [256, (512, 256)])
+def test_fused_untile_apply_matches_unfused(pdt, cuda_graph, tile):
     """The fused untile (WD/LR applied in place, inside the graph) leaves the
     parameters bit-identical to the unfused path (update tensors, then the
     WD/LR pass), over several steps with an lr/wd change between steps, which
-    the fused path reads from its device table without a recapture."""
-    shapes = [(512, 1024), (256, 512), (700, 300)]
+    the fused path reads from its device table without a recapture. Three
+    param groups with their own lr/wd; wide, square and tall tiles (the
+    transposed untile), ragged edges and full-matrix NS groups."""
+    shapes = [(512, 1024), (256, 512), (700, 300), (300, 100), (100, 300), (1024, 512)]
+    settings = [(0.02, 0.05), (0.01, 0.0), (0.03, 0.2)]
     m_f = make_model(shapes, pdt)
     m_u = copy.deepcopy(m_f)
-    kw = dict(lr=0.02, weight_decay=0.05, tile_size=256, cuda_graph=cuda_graph, cuda_graph_warmup=2)
-    o_f = HiMuon(muon_groups(m_f, wd=0.05), **kw)
-    o_u = HiMuon(muon_groups(m_u, wd=0.05), **kw)
+
+    def groups(m):
+        ps = list(m.parameters())
+        return [{"params": ps[2 * i: 2 * i + 2], "lr": lr, "weight_decay": wd, "use_muon": True}
+                for i, (lr, wd) in enumerate(settings)]
+
+    m_r = copy.deepcopy(m_f)
+    kw = dict(tile_size=tile, cuda_graph=cuda_graph, cuda_graph_warmup=2)
+    o_f = HiMuon(groups(m_f), **kw)
+    o_u = HiMuon(groups(m_u), **kw)
     o_u._fuse_untile = False
+    # referee: eager, unfused (WD/LR by the reference's torch ops)
+    o_r = HiMuon(groups(m_r), **{**kw, "cuda_graph": False})
+    o_r._fuse_untile = False
+    runs = ((m_f, o_f), (m_u, o_u), (m_r, o_r))
     for k in range(7):
         if k == 5:
-            for o in (o_f, o_u):
+            for _, o in runs:
                 o.param_groups[0]["lr"] = 0.01
                 o.param_groups[0]["weight_decay"] = 0.1
-        seed_grads(m_f, 400 + k)
-        seed_grads(m_u, 400 + k)
-        o_f.step()
-        o_u.step()
+                o.param_groups[2]["weight_decay"] = 0.0
+        for m, o in runs:
+            seed_grads(m, 400 + k)
+            o.step()
     assert all(g["tiles"].fused for g in o_f._groups)
     assert not any(g["tiles"].fused for g in o_u._groups)
+    assert any(g["tiles"].tile_h > g["tiles"].tile_w for g in o_f._groups)  # transposed untile ran
     if cuda_graph:
         assert o_f._cuda_graph is not None and o_f._pending_updates
         assert all(u is None for _, u, _ in o_f._pending_updates)
-    for a, b in zip(m_f.parameters(), m_u.parameters()):
-        assert torch.equal(a, b)
+    bad = []
+    for name, m in (("fused", m_f), ("unfused", m_u)):
+        for i, (a, r) in enumerate(zip(m.parameters(), m_r.parameters())):
+            if not torch.equal(a, r):
+                bad.append((name, i, tuple(a.shape), int((a != r).sum()), float((a.float() - r.float()).abs().max())))
+    assert not bad, bad
 
 
 # ---------------------------------------------------------------------------
