@@ -263,6 +263,46 @@ def test_ns5_sub_batch_invariance(ns_family):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
 
 
+STALE_SHAPES = [
+    # (label, n, M, N): one per kernel family / geometry class
+    ("lds_128", 3, 128, 128),
+    ("lds_100x200", 3, 100, 200),
+    ("blk_100x300", 3, 100, 300),
+    ("blk_tall_300x100", 3, 300, 100),
+    ("blk_300x300", 2, 300, 300),
+    ("stream_256", 3, 256, 256),
+    ("stream_200x500", 2, 200, 500),
+    ("stream_tall_1000x400", 2, 1000, 400),
+]
+
+
+@pytest.mark.parametrize("label,n,M,N", STALE_SHAPES, ids=[s[0] for s in STALE_SHAPES])
+def test_ns5_ignores_stale_buffer_contents(label, n, M, N, ns_family):
+    """The tile buffers and the NS workspace come from torch.empty: every
+    element any kernel reads must have been written earlier in the same step.
+    NaN-filled buffers must give bit-for-bit the result of zero-filled ones."""
+    print(f"[ns5 stale] {label} {ns_family}", flush=True)
+    G = _cpu_randn((n, M, N), seed=M + N, scale=1e-3).to(torch.bfloat16).to(DEV)
+    outs = []
+    for fill in (0.0, float("nan")):
+        flat = G.reshape(-1, N)
+        grp = TileGroup([flat], [flat], [None], M, N, [1.0], [0.0], [False], torch.device(DEV), torch.bfloat16)
+        sb = grp.default_sub_batch()
+        ws = torch.empty(max(2, grp.workspace_bytes(sb)), device=DEV, dtype=torch.uint8)
+        grp.tiles.fill_(fill)
+        grp.alt.fill_(fill)
+        ws.view(torch.bfloat16).fill_(fill)
+        grp.updates[0].fill_(fill)
+        grp.gather()
+        grp.ns(0, grp.n_tiles, 5, ws, sb)
+        grp.untile(5)
+        outs.append(grp.updates[0].clone())
+    assert torch.isfinite(outs[1].float()).all()
+    assert torch.equal(outs[0], outs[1])
+    err = per_tile_rel_fro(outs[1].view(n, M, N).float(), ns5_torch_staged(G).float())
+    assert err.max() <= 2e-2, err
+
+
 def test_ns5_workspace_too_small_raises():
     G = _cpu_randn((2, 128, 128), seed=1).to(DEV)
     grp = TileGroup([G.view(-1, 128)], [G.view(-1, 128)], [None], 128, 128, [1.0], [0.0], [False],
