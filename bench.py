@@ -38,12 +38,26 @@ PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 4096 FLOP/clk x 2.
 # NS stage kernels per kernel family (HIMUON_NS_PATH), per NS iteration.
 NS_KERNELS = {
     "stream": "ns5 stage: ns_st_kernel<0> (X X^T), <1> (c A A^T + b A), <2> (B X + a X) per iteration",
+    "lds": "ns5 stage: ns5_lds_kernel (all 5 iterations of a 128-row tile resident in LDS)",
     "small": "ns5 stage: ns_gram_kernel x2 + ns_apply_kernel per iteration",
 }
 
 
 def ns_path() -> str:
     return os.environ.get("HIMUON_NS_PATH", "stream")
+
+
+def ns_family(mp: int, np_: int) -> str:
+    """The NS kernel family the library runs for an (mp, np) tile buffer
+    (himuon_ns5's dispatch): LDS-resident for mp == 128 and np <= 256,
+    streamed 256-blocks for edges that are multiples of 256, else 128-blocks."""
+    if ns_path() == "small":
+        return "small"
+    if mp == 128 and np_ in (128, 256):
+        return "lds"
+    if mp % 256 == 0 and np_ % 256 == 0:
+        return "stream"
+    return "small"
 
 
 PEAK_HBM_GBS = 8000.0
@@ -252,7 +266,18 @@ def cpu_baseline(layers, shapes, tile, budget_s: float = 20.0):
     budget), scaled to one full step. Returns the cpu_baseline JSON object."""
     from oracle import himuon_oracle as O
 
-    threads = os.cpu_count() or 1
+    # threads OpenBLAS runs with (its own variable, else OMP_NUM_THREADS, else all cores)
+    threads = int(os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    threads = min(threads, os.cpu_count() or threads)
+    cpu_model, bf16 = platform.processor() or platform.machine(), False
+    try:
+        with open("/proc/cpuinfo") as f:
+            info = f.read()
+        names = [ln.split(":", 1)[1].strip() for ln in info.splitlines() if ln.startswith("model name")]
+        cpu_model = names[0] if names else cpu_model
+        bf16 = " avx512_bf16" in info or " amx_bf16" in info
+    except OSError:
+        pass
     rng = np.random.default_rng(0)
     done_tiles = 0
     total_tiles = 0
@@ -299,8 +324,10 @@ def cpu_baseline(layers, shapes, tile, budget_s: float = 20.0):
         "cores": threads,
         "kind": "port",
         "sample": f"oracle/himuon_oracle.py numpy (OpenBLAS sgemm, bf16-staged NS5) on {done_tiles} of "
-                  f"{total_tiles} tiles ({t_spent:.1f} s); NS time per tile x all tiles; "
-                  f"cpu={platform.processor() or platform.machine()}",
+                  f"{total_tiles} tiles ({t_spent:.1f} s); NS time per tile x all tiles",
+        "cpu": cpu_model,
+        "cpu_native_bf16": bf16,
+        "arith": "fp32 sgemm with bf16 rounding between stages (no bf16 GEMM on the CPU path)",
     }
 
 
@@ -358,13 +385,22 @@ def main():
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     ev_ms = e0.elapsed_time(e1) / args.steps
+    # per-step distribution (HIP events around each step), after the timed loop
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    marks[0].record(s)
+    for k in range(args.steps):
+        opt.step()
+        marks[k + 1].record(s)
+    torch.cuda.synchronize()
+    per_step = np.array([marks[k].elapsed_time(marks[k + 1]) for k in range(args.steps)])
 
     ns_ms = time_ns_stage(opt, reps=max(3, args.steps // 2))
     gather_ms, untile_ms = time_io_stage(opt, reps=max(3, args.steps // 2))
     apply_ms = time_apply(opt, reps=max(3, args.steps // 2))
     flops = algorithmic_flops(opt)
     n_tiles = sum(g["tiles"].n_tiles for g in opt._groups)
-    traffic = NS5_STAGE_TRAFFIC_BYTES.get(args.config) if ns_path() == "stream" else None
+    fams = sorted({ns_family(g["tiles"].mp, g["tiles"].np) for g in opt._groups})
+    traffic = NS5_STAGE_TRAFFIC_BYTES.get(args.config) if fams == ["stream"] else None
     n_el = sum(p.numel() for p in params)
     # bytes per element: update (untile writes it, the WD/LR pass reads it), parameter;
     # fused: the untile reads the NS tile and reads and writes the parameter
@@ -397,6 +433,7 @@ def main():
             "param_dtype": str(pdtype).replace("torch.", ""),
         },
         "step_ms_events": round(ev_ms, 3),
+        "step_ms_p25_p50_p75": [round(float(v), 3) for v in np.percentile(per_step, [25, 50, 75])],
         "ns5_ms": round(ns_ms, 3),
         "ns5_tflops": round(ns_tflops, 1),
         "ns5_frac_peak": round(ns_tflops / PEAK_BF16_TFLOPS, 4),
@@ -409,7 +446,7 @@ def main():
         "apply_gbs": None if fused else round((2 * pb + ub) * n_el / (apply_ms * 1e-3) / 1e9, 1),
         "update_dtype": None if fused else str(opt._groups[0]["tiles"].upd_dtype).replace("torch.", ""),
         "roofline": {
-            "kernel": NS_KERNELS.get(ns_path(), ns_path()),
+            "kernel": "; ".join(NS_KERNELS[f] for f in fams),
             "bound": "mfma",
             "achieved": round(ns_tflops, 1),
             "peak": PEAK_BF16_TFLOPS,
