@@ -9,8 +9,11 @@
 // values torch's two elementwise kernels compute in fp32 opmath: the in-place
 // add first rounds `other` to the parameter's dtype (a no-op for fp32
 // parameters), then evaluates `self + alpha * other` as one fused
-// multiply-add (verified bit for bit against torch on the GPU). With wd == 0
-// the first line is the identity, as the reference's skipped mul_.
+// multiply-add (verified bit for bit against torch on the GPU). For fp16
+// parameters with an fp32 update torch's mixed-dtype add rounds that
+// multiply-add once from the exact value instead of through fp32
+// (fma_f16_once, measured over 1 M elements); other pairs go through fp32.
+// With wd == 0 the first line is the identity, as the reference's skipped mul_.
 //
 // HBM-bound: read p, read u, write p (8 B per element for bf16 params and
 // fp32 updates, against 12 B for the two separate torch passes). Work is cut
@@ -53,6 +56,15 @@ HM_DEV int find_desc(const HimuonApplyDesc* __restrict__ d, int n, int64_t q) {
   return lo;
 }
 
+// p1 + alpha * round_p(u), stored in the parameter dtype PD (see above).
+template <int PD, int UD>
+HM_DEV float add_update(float alpha, float u, float p1) {
+  if constexpr (PD == HIMUON_DTYPE_F16 && UD == HIMUON_DTYPE_F32)
+    return fma_f16_once(alpha, round_to<PD>(u), p1);
+  else
+    return __builtin_fmaf(alpha, round_to<PD>(u), p1);
+}
+
 template <int PD, int UD>
 __global__ __launch_bounds__(kThreads) void apply_kernel(const HimuonApplyDesc* __restrict__ descs,
                                                          int n_descs, int64_t n_chunks,
@@ -78,12 +90,12 @@ __global__ __launch_bounds__(kThreads) void apply_kernel(const HimuonApplyDesc* 
       if (e0 >= D.numel) continue;
       if (e0 + 8 <= D.numel) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) p[h][e] = __builtin_fmaf(alpha, round_to<PD>(u[h][e]), round_to<PD>(p[h][e] * s));
+        for (int e = 0; e < 8; ++e) p[h][e] = add_update<PD, UD>(alpha, u[h][e], round_to<PD>(p[h][e] * s));
         store8<PD>(D.param, e0, p[h]);
       } else {
         for (int64_t e = e0; e < D.numel; ++e) {
           const float p1 = round_to<PD>(load_elem<PD>(D.param, e) * s);
-          store_elem<PD>(D.param, e, __builtin_fmaf(alpha, round_to<PD>(load_elem<UD>(D.update, e)), p1));
+          store_elem<PD>(D.param, e, add_update<PD, UD>(alpha, load_elem<UD>(D.update, e), p1));
         }
       }
     }

@@ -53,6 +53,19 @@ HM_DEV uint16_t f32_to_f16(float f) {
   return (uint16_t)(sign | (q + ((rem > half) || (rem == half && (q & 1u)))));
 }
 
+// p + alpha * u rounded ONCE to fp16 (u and p already fp16 values): torch's
+// in-place add of an fp32 tensor into an fp16 one evaluates it as a fused
+// mixed-precision multiply-add with a single rounding. The exact value
+// (a 35-bit product plus an fp16 term) is formed in double; converting it to
+// fp32 with round-to-odd and then to fp16 with round-to-nearest-even rounds it
+// once, since fp32 keeps more than two bits beyond fp16's precision.
+HM_DEV float fma_f16_once(float alpha, float u, float p) {
+  const double t = __builtin_fma((double)alpha, (double)u, (double)p);
+  float r = __double2float_rz(t);
+  if ((double)r != t) r = __uint_as_float(__float_as_uint(r) | 1u);
+  return f16_to_f32(f32_to_f16(r));
+}
+
 // Load / store one element of a gradient-typed tensor as fp32.
 template <int DT>
 HM_DEV float load_elem(const void* p, int64_t i) {

@@ -24,14 +24,15 @@ from . import _native as nat
 def update_dtype(params, grad_dtype: torch.dtype) -> torch.dtype:
     """Storage dtype of a group's update tensors. The update's only consumer
     is the WD/LR application, which (as torch's in-place add does) first rounds
-    it to the parameter dtype; when every parameter of the group has one dtype
-    narrower than fp32 grads, storing the update already rounded to it gives
-    the same parameters bit for bit and moves 2 bytes per element instead of 4."""
+    it to the parameter dtype; when every parameter of the group is bf16 and
+    the grads are fp32, storing the update already rounded to bf16 gives the
+    same parameters bit for bit and moves 2 bytes per element instead of 4.
+    Not for fp16 parameters: torch adds an fp32 update into them with one
+    rounding from the exact value, an fp16 update through fp32 (two), so the
+    stored dtype would change the result."""
     pdts = {p.dtype for p in params}
-    if grad_dtype == torch.float32 and len(pdts) == 1:
-        (pd,) = pdts
-        if pd in (torch.bfloat16, torch.float16):
-            return pd
+    if grad_dtype == torch.float32 and pdts == {torch.bfloat16}:
+        return torch.bfloat16
     return grad_dtype
 
 

@@ -461,13 +461,17 @@ class HiMuon(Optimizer):
     def _build_groups(self, plan: list[dict]) -> list[dict]:
         group_to_idx = {id(g): i for i, g in enumerate(self.param_groups)}
 
-        def fusable(params, gidx) -> bool:
+        def fusable(params, gidx, grad_dtype) -> bool:
             # The untile applies WD/LR in place: one parameter dtype the kernels
             # take, row-major 2-D parameters, group indices inside the table.
+            # fp16 parameters not with fp32 grads: the fused untile adds the
+            # update through fp32; torch adds an fp32 update into fp16 with one
+            # rounding, which the WD/LR pass reproduces.
             pd = {p.dtype for p in params}
             return (
                 self._fuse_untile
                 and len(pd) == 1 and next(iter(pd)) in nat.DTYPE_CODES
+                and (next(iter(pd)) != torch.float16 or grad_dtype != torch.float32)
                 and all(p.is_cuda and p.ndim == 2 and (p.stride(1) == 1 or p.shape[1] == 1) for p in params)
                 and max(gidx) < nat.APPLY_MAX_GROUPS
             )
@@ -492,7 +496,7 @@ class HiMuon(Optimizer):
                 device=params[0].grad.device,
                 dtype=dtype,
                 upd_dtype=update_dtype(params, dtype),
-                apply_groups=gidx if fusable(params, gidx) else None,
+                apply_groups=gidx if fusable(params, gidx, dtype) else None,
             )
             self._concat_buffers[bucket["bucket_key"]] = grp.tiles
             out.append(
@@ -523,7 +527,7 @@ class HiMuon(Optimizer):
                 device=params[0].grad.device,
                 dtype=dtype,
                 upd_dtype=update_dtype(params, dtype),
-                apply_groups=gidx if fusable(params, gidx) else None,
+                apply_groups=gidx if fusable(params, gidx, dtype) else None,
             )
             out.append(
                 {

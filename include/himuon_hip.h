@@ -170,7 +170,9 @@ int himuon_untile(const HimuonParamDesc* params_dev, int n_params,
  * read from DEVICE memory when the kernel runs, so a captured graph picks up
  * learning-rate and weight-decay changes written there before each replay.
  * The parameters end exactly as himuon_untile followed by
- * himuon_apply_updates would leave them. Replaces the untile plus the
+ * himuon_apply_updates would leave them when the update dtype is the
+ * parameter dtype (the fma runs in fp32; for fp16 parameters with fp32
+ * grads use the two-pass path, whose update-into-fp16 add rounds once). Replaces the untile plus the
  * outside-graph WD/LR of the Muon parameters (himuon.py:315-348, 215-228).
  */
 int himuon_untile_apply(const HimuonParamDesc* params_dev, int n_params,
@@ -201,6 +203,9 @@ int himuon_write_scale_alpha(float* scale_alpha_dev, const float* scale_by_group
  * update must be contiguous and 16-byte aligned. For every element:
  *     p1 = round_p(float(p) * scale[group]);          p.mul_(1 - lr*wd)
  *     p  = round_p(fma(alpha[group], round_p(u), p1)) p.add_(u, alpha=-lr)
+ * with the fma in fp32, except for fp16 parameters with an fp32 update,
+ * where (as torch's mixed-dtype add does) p1 + alpha * round_p(u) is rounded
+ * to fp16 once from its exact value.
  * scale_by_group / alpha_by_group are HOST arrays of n_groups floats (copied
  * into the launch), so lr and wd may change every step without re-recording.
  * One launch covers the descriptors of one (param dtype, update dtype) pair.

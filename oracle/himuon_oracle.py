@@ -49,8 +49,9 @@ ns5_eager against ns5_fp64 (bf16-sized distance) and the singular-value band;
 fma32 against exact rational arithmetic; apply_update against torch's CPU ops
 for fp32 params (bit-exact) and, in tests/test_gpu_apply.py, against torch's
 GPU ops for bf16 and fp32 params (each element equals torch's bulk form or its
-remainder form). fp16 params against torch: parity unpinned (no configuration
-uses them). lerp32 against torch's CPU lerp (both weight branches,
+remainder form) and for fp16 params over torch's vectorised bulk path
+(bit-exact; torch's non-vectorised tail rounds a few fp16 elements by neither
+form). lerp32 against torch's CPU lerp (both weight branches,
 bit-exact); adamw_step against torch's CPU ops: bf16 moments and update and
 fp32 moments bit-exact (torch's CPU fp32 sqrt is not correctly rounded, so
 the fp32 update is pinned within 2 ulp there), adamw_bias against its
@@ -347,15 +348,24 @@ def lr_scale(block_shape, lr_adjust: str = "tile") -> float:
     return 0.2 * math.sqrt(max(block_shape[0], block_shape[1]))
 
 
-def apply_update(p, update, lr: float, wd: float, dtype: str = "float32") -> np.ndarray:
+def apply_update(p, update, lr: float, wd: float, dtype: str = "float32",
+                 update_dtype: str = "float32") -> np.ndarray:
     """p.mul_(1 - lr*wd) (if wd > 0), then p.add_(update, alpha=-lr), each
     stored in the parameter dtype (himuon.py:222-228, 345-348). torch's
     in-place add computes in the parameter's dtype: the update is first
-    rounded to it, then `p + alpha * u` is one fp32 fused multiply-add."""
+    rounded to it, then `p + alpha * u` is one fp32 fused multiply-add. For
+    fp16 parameters with an fp32 update (the optimizer's fp32 grads) torch's
+    mixed-dtype add rounds that multiply-add once from the exact value
+    instead of through fp32 (measured on the GPU over 1 M elements); numpy's
+    float64 -> float16 conversion is that single rounding, and the float64
+    value is exact (a 35-bit product plus an fp16 term)."""
     p = np.asarray(p, dtype=F32)
     if wd > 0.0:
         p = round_to(p * F32(1 - lr * wd), dtype)
     u = round_to(np.asarray(update, dtype=F32), dtype)
+    if dtype == "float16" and update_dtype == "float32":
+        exact = np.float64(F32(-lr)) * u.astype(np.float64) + p.astype(np.float64)
+        return exact.astype(np.float16).astype(F32)
     return round_to(fma32(F32(-lr), u, p), dtype)
 
 
@@ -447,5 +457,5 @@ def step_param(op: OracleParam, ns=ns5_staged):
         scale = lr_scale((th, tw), op.lr_adjust)
     # update tensor in grad dtype, scaled in-graph (himuon.py:257, 338-341)
     upd = round_to(round_to(u, op.g_dtype) * F32(scale), op.g_dtype)
-    newp = apply_update(op.p, upd, op.lr, op.wd, op.p_dtype)
+    newp = apply_update(op.p, upd, op.lr, op.wd, op.p_dtype, op.g_dtype)
     return newp, nb, upd

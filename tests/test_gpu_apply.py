@@ -66,7 +66,7 @@ def test_apply_bit_exact_vs_oracle_within_ulp_of_torch(pdt, udt):
         r = p0.clone().to(DEV)
         _reference(r, u_dev, *groups[gi])
         ref.append(r)
-        o = O.apply_update(p0.float().numpy(), u0.float().numpy(), *groups[gi], NAMES[pdt])
+        o = O.apply_update(p0.float().numpy(), u0.float().numpy(), *groups[gi], NAMES[pdt], NAMES[udt])
         lr, wd = groups[gi]
         p1 = O.round_to(p0.float().numpy() * np.float32(1 - lr * wd), NAMES[pdt]) if wd > 0 else p0.float().numpy()
         o_rem = O.round_to(O.fma32(np.float32(-lr), u0.float().numpy(), p1), NAMES[pdt])
@@ -79,12 +79,16 @@ def test_apply_bit_exact_vs_oracle_within_ulp_of_torch(pdt, udt):
     torch.cuda.synchronize()
     for (p, _, _), r, (w, w_rem) in zip(entries, ref, want):
         assert (_bits(p.data) == _bits(w)).all(), (pdt, udt, tuple(p.shape))
-        torch_ok = (_bits(r) == _bits(w)) | (_bits(r) == _bits(w_rem))
         if pdt != torch.float16:
-            # fp16 parameters (no config uses them): some elements of torch's
-            # result follow neither form; parity against torch is unpinned
-            # for them (kernel == oracle still holds above).
+            # every element of torch's result is its bulk form (the oracle's) or
+            # its remainder form (the update not rounded first)
+            torch_ok = (_bits(r) == _bits(w)) | (_bits(r) == _bits(w_rem))
             assert torch_ok.all(), (pdt, udt, tuple(p.shape))
+        # fp16 parameters with an fp32 update: torch's mixed-dtype add rounds once
+        # from the exact value over a large tensor (the oracle's form, pinned by
+        # test_oracle_apply_matches_torch_gpu on 1 << 20 elements), but its
+        # small-launch path rounds these ragged small shapes by yet other forms;
+        # no configuration has fp16 parameters. Kernel == oracle holds above.
 
 
 def test_apply_non_contiguous_falls_back():
@@ -94,7 +98,8 @@ def test_apply_non_contiguous_falls_back():
     assert len(tables.fallback) == 1 and not tables.launches
 
 
-@pytest.mark.parametrize("pdt,name", [(torch.bfloat16, "bfloat16"), (torch.float32, "float32")])
+@pytest.mark.parametrize("pdt,name", [(torch.bfloat16, "bfloat16"), (torch.float32, "float32"),
+                                      (torch.float16, "float16")])
 @pytest.mark.parametrize("udt", [torch.float32, torch.bfloat16])
 def test_oracle_apply_matches_torch_gpu(pdt, name, udt):
     """Pins oracle.apply_update on the reference's own platform: torch's GPU
@@ -108,11 +113,11 @@ def test_oracle_apply_matches_torch_gpu(pdt, name, udt):
     for lr, wd in [(1e-2, 0.1), (3e-3, 0.0)]:
         r = p0.clone().to(DEV)
         _reference(r, u0.to(DEV), lr, wd)
-        got = O.apply_update(p0.float().numpy(), u0.float().numpy(), lr, wd, name)
+        got = O.apply_update(p0.float().numpy(), u0.float().numpy(), lr, wd, name, NAMES[udt])
         assert (got == r.float().cpu().numpy()).all(), (name, udt, lr, wd)
 
 
-@pytest.mark.parametrize("pdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("pdt", [torch.bfloat16])
 def test_narrow_update_storage_gives_identical_params(pdt):
     """The optimizer stores a bucket's update in the parameters' dtype when
     that is narrower than the fp32 grads (engine.update_dtype): the WD/LR
@@ -126,6 +131,8 @@ def test_narrow_update_storage_gives_identical_params(pdt):
     grads = [(torch.randn(*s, generator=gen) * 1e-3).to(DEV) for s in shapes]
     assert update_dtype(params, torch.float32) == pdt
     assert update_dtype(params, torch.bfloat16) == torch.bfloat16
+    # fp16 parameters keep fp32 updates (torch rounds an fp32 update into them once)
+    assert update_dtype([p.half() for p in params], torch.float32) == torch.float32
     assert update_dtype([params[0], params[1].float()], torch.float32) == torch.float32
     results = []
     for udt in (torch.float32, pdt):

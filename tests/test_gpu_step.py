@@ -124,7 +124,7 @@ def test_update_tensor_matches_oracle_per_tile():
             assert e < 2e-2, (r, c, e)
 
 
-@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("cuda_graph", [False, True])
 @pytest.mark.parametrize("tile", [256, (512, 256)])
 def test_fused_untile_apply_matches_unfused(pdt, cuda_graph, tile):
@@ -168,11 +168,27 @@ def test_fused_untile_apply_matches_unfused(pdt, cuda_graph, tile):
     if cuda_graph:
         assert o_f._cuda_graph is not None and o_f._pending_updates
         assert all(u is None for _, u, _ in o_f._pending_updates)
-    bad = []
-    for name, m in (("fused", m_f), ("unfused", m_u)):
-        for i, (a, r) in enumerate(zip(m.parameters(), m_r.parameters())):
+    def diffs(m, ref):
+        out = []
+        for i, (a, r) in enumerate(zip(m.parameters(), ref.parameters())):
             if not torch.equal(a, r):
-                bad.append((name, i, tuple(a.shape), int((a != r).sum()), float((a.float() - r.float()).abs().max())))
+                out.append((i, tuple(a.shape), int((a != r).sum()), a.numel(),
+                            float((a.float() - r.float()).abs().max())))
+        return out
+
+    if pdt == torch.float16:
+        # torch's fp16 p.add_(u, alpha=-lr) is p + alpha*u as one fp32 fma (the form
+        # the kernels use) in its vectorised bulk path, measured bit for bit on the
+        # GPU, but not in the non-vectorised tail of each launch, which rounds some
+        # elements differently by 1 ulp. The tail covers the same elements every
+        # step, so over 7 steps those drift by a few ulp. Against torch's ops (the
+        # referee, and the unfused path's eager warm-up steps): at most 0.1 % of
+        # the elements, by at most 1e-3 (parameters ~0.05).
+        for name, m in (("fused", m_f), ("unfused", m_u)):
+            for i, shape, n_bad, n, dmax in diffs(m, m_r):
+                assert n_bad <= 1e-3 * n and dmax <= 1e-3, (name, i, shape, n_bad, dmax)
+        return
+    bad = [("fused",) + d for d in diffs(m_f, m_r)] + [("unfused",) + d for d in diffs(m_u, m_r)]
     assert not bad, bad
 
 
@@ -211,6 +227,56 @@ def test_eager_matches_graph():
     assert o_g._cuda_graph is not None
     for a, b in zip(m_e.parameters(), m_g.parameters()):
         assert torch.equal(a, b)
+
+
+def test_fp16_params_fp32_grads_eager_matches_graph():
+    """fp16 parameters with fp32 grads: the update stays fp32 and is not
+    fused into the untile; eagerly the reference's torch ops add it, under
+    replay the HIP WD/LR pass does, rounding p + alpha * u once from the exact
+    value as torch's mixed-dtype add does over a large tensor: bit-identical
+    for the 512 x 1024 parameter. torch takes other rounding forms on smaller
+    tensors (measured: 0.8 % and 6 % of the elements of the 700 x 300 and
+    300 x 100 parameters, 1 ulp), bounded here."""
+    shapes = [(512, 1024), (700, 300), (300, 100)]
+    gen = torch.Generator().manual_seed(5)
+    base = [(torch.randn(*s, generator=gen) * 0.02).half() for s in shapes]
+
+    def params():
+        ps = []
+        for b in base:
+            p = torch.nn.Parameter(b.clone().to(DEV))
+            p.grad_dtype = torch.float32
+            ps.append(p)
+        return ps
+
+    def groups(ps):
+        return [{"params": ps[:1], "lr": 0.02, "weight_decay": 0.1, "use_muon": True},
+                {"params": ps[1:], "lr": 0.01, "weight_decay": 0.05, "use_muon": True}]
+
+    p_e, p_g = params(), params()
+    o_e = HiMuon(groups(p_e), tile_size=256, cuda_graph=False)
+    o_g = HiMuon(groups(p_g), tile_size=256, cuda_graph=True, cuda_graph_warmup=2)
+    for k in range(6):
+        g = torch.Generator().manual_seed(300 + k)
+        for a, b in zip(p_e, p_g):
+            v = (torch.randn(a.shape, generator=g) * 1e-3).to(DEV)
+            for p in (a, b):
+                if p.grad is None:
+                    p.grad = torch.empty_like(v)
+                p.grad.copy_(v)
+        o_e.step()
+        o_g.step()
+    assert o_g._cuda_graph is not None
+    assert not any(grp["tiles"].fused for grp in o_g._groups)
+    assert all(grp["tiles"].upd_dtype == torch.float32 for grp in o_g._groups)
+    rep = [(tuple(a.shape), int((a != b).sum()), a.numel(), float((a.float() - b.float()).abs().max()))
+           for a, b in zip(p_e, p_g)]
+    for a, b in zip(p_e, p_g):
+        assert a.dtype == torch.float16
+        if a.numel() >= 1 << 19:
+            assert torch.equal(a, b), rep
+        else:
+            assert (a.float() - b.float()).abs().max() <= 1.3e-4, rep  # 1-2 fp16 ulp at |p| < 0.1
 
 
 def test_graph_replays_track_lr_schedule():
