@@ -455,6 +455,10 @@ def main():
             "traffic": traffic,
             "traffic_gbs": round(traffic / (ns_ms * 1e-3) / 1e9, 1) if traffic else None,
             "traffic_frac_hbm_peak": round(traffic / (ns_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if traffic else None,
+            # measured arithmetic intensity against the ridge point (peak FLOP/s / peak B/s):
+            # below the ridge the measured traffic, not the MFMA rate, bounds the stage
+            "intensity_flop_per_byte": round(flops / traffic, 1) if traffic else None,
+            "ridge_flop_per_byte": round(PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9), 1),
         },
     }
     if args.reconfigure:
