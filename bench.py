@@ -6,11 +6,15 @@ TFLOP/s and its fraction of the bf16 dense MFMA peak.
 Default workload: the Qwen3-4B-shaped parameter set (36 layers x {q 4096x2560,
 k/v 1024x2560, o 2560x4096, gate/up 9728x2560, down 2560x9728}), bf16 params,
 fp32 grads ~N(0, 1e-3^2), tile_size=512 (13,860 tiles), the whole step
-captured in a hipGraph (LR/WD applied outside it, as the reference does).
-Inputs are synthetic and resident in HBM before the timed region.
+captured in a hipGraph. Inputs are synthetic and resident in HBM before the
+timed region.
 
-A "step" is one ``optimizer.step()``: graph replay (momentum + gather ->
-normaliser -> NS5 -> untile) plus the outside-graph WD/LR application.
+A "step" is one ``optimizer.step()``: the write of the groups' (1 - lr*wd,
+-lr) into the device table the graph reads (LR schedules need no recapture,
+as with the reference's outside-graph WD/LR), then graph replay (momentum +
+gather -> normaliser -> NS5 -> untile applying WD/LR to the parameters), then
+the outside-graph WD/LR pass for anything the untile did not take (nothing in
+the default workload). Defaults: 20 warm-up steps, 50 timed steps.
 
     python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline] [--no-adamw]
                    [--reconfigure T]
@@ -334,8 +338,8 @@ def cpu_baseline(layers, shapes, tile, budget_s: float = 20.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-adamw", action="store_true",
