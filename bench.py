@@ -351,8 +351,9 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print(json.dumps({"error": "this build runs the HiMuon step on one GPU only; "
-                                   "--gpus N > 1 is not supported (see DESIGN.md, sharding)"}))
+        print(json.dumps({"error": "this build runs the HiMuon step on one GPU only; --gpus N > 1 is not "
+                                   "supported (multi-GPU would shard the tiles and all-gather the updated "
+                                   "parameter rows; not built)"}))
         sys.exit(2)
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no ROCm device"}))

@@ -1,0 +1,47 @@
+"""bench.py's host-side logic (CPU): the NS kernel family named in the
+roofline for each tile geometry, and the single-GPU guard."""
+
+from __future__ import annotations
+
+import json
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+
+
+def test_ns_family_follows_the_library_dispatch(monkeypatch):
+    monkeypatch.delenv("HIMUON_NS_PATH", raising=False)
+    # LDS-resident kernel: mp == 128 and np <= 256
+    assert bench.ns_family(128, 128) == "lds"
+    assert bench.ns_family(128, 256) == "lds"
+    # streamed 256-blocks: both padded edges multiples of 256
+    assert bench.ns_family(512, 512) == "stream"
+    assert bench.ns_family(256, 1024) == "stream"
+    assert bench.ns_family(1024, 3072) == "stream"
+    # everything else: 128-block kernels
+    assert bench.ns_family(128, 384) == "small"
+    assert bench.ns_family(640, 768) == "small"
+    assert bench.ns_family(384, 384) == "small"
+    monkeypatch.setenv("HIMUON_NS_PATH", "small")
+    assert bench.ns_family(512, 512) == "small"
+    assert set(bench.NS_KERNELS) == {"stream", "lds", "small"}
+
+
+def test_ns_flops_is_the_normative_count():
+    # 5 (4 m^2 n + 2 m^3), m <= n: 30 T^3 for a square tile
+    assert bench.ns_flops(512, 512) == 30 * 512**3
+    assert bench.ns_flops(128, 128) == 30 * 128**3
+    assert bench.ns_flops(1024, 2048) == 5 * (4 * 1024**2 * 2048 + 2 * 1024**3)
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    msg = json.loads(r.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"]
