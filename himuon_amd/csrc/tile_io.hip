@@ -18,7 +18,11 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kSlabElems = 16384;  // NS elements per gather/untile work item (plain tiles)
-constexpr int kVec = 8;      // 8-element vectors per thread per load batch
+constexpr int kVec = 8;      // 8-element vectors per thread per load batch (untile)
+// The plain-tile gather loads grad and momentum vectors: 4 per batch keep it
+// at about 150 VGPRs (three workgroups per CU); 8 took all 256 and measured
+// 3-6 % slower. Each thread still sums the same elements in the same order.
+constexpr int kGatherVec = 4;
 constexpr int kBlk = 64;     // NS block edge for the transposed variants
 constexpr int kBlkPitch = kBlk + 8;
 
@@ -83,12 +87,12 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
     const bool nesterov = P.nesterov != 0;
     uint16_t* out = tiles + t * (int64_t)geo.mp * geo.np;
     float ssq = 0.f;
-    for (int v0 = 0; v0 < per_item; v0 += kThreads * kVec) {
-      float g[kVec][8], m[kVec][8];
-      bool fast[kVec];
+    for (int v0 = 0; v0 < per_item; v0 += kThreads * kGatherVec) {
+      float g[kGatherVec][8], m[kGatherVec][8];
+      bool fast[kGatherVec];
       // Phase 1: every load of the batch is issued before any is used.
 #pragma unroll
-      for (int k = 0; k < kVec; ++k) {
+      for (int k = 0; k < kGatherVec; ++k) {
         const int v = v0 + k * kThreads + threadIdx.x;
         const int i = q * rows + v / vpr, j0 = (v % vpr) * 8;
         const int64_t pr = (int64_t)r * geo.tile_h + i, pc = (int64_t)c * geo.tile_w + j0;
@@ -102,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
       }
       // Phase 2: momentum, momentum store, bf16 NS operand store.
 #pragma unroll
-      for (int k = 0; k < kVec; ++k) {
+      for (int k = 0; k < kGatherVec; ++k) {
         const int v = v0 + k * kThreads + threadIdx.x;
         if (v >= per_item) continue;
         const int i = q * rows + v / vpr, j0 = (v % vpr) * 8;
