@@ -39,7 +39,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 4096 FLOP/clk x 2.4 GHz)
 
-# NS stage kernels per kernel family (HIMUON_NS_PATH), per NS iteration.
+# NS stage kernels per kernel family, per NS iteration.
 NS_KERNELS = {
     "stream": "ns5 stage: ns_st_kernel<0> (X X^T), <1> (c A A^T + b A), <2> (B X + a X) per iteration",
     "lds": "ns5 stage: ns5_lds_kernel (all 5 iterations of a 128-row tile resident in LDS)",
@@ -47,15 +47,12 @@ NS_KERNELS = {
 }
 
 
-def ns_path() -> str:
-    return os.environ.get("HIMUON_NS_PATH", "stream")
-
-
-def ns_family(mp: int, np_: int) -> str:
+def ns_family(mp: int, np_: int, family: str = "auto") -> str:
     """The NS kernel family the library runs for an (mp, np) tile buffer
-    (himuon_ns5's dispatch): LDS-resident for mp == 128 and np <= 256,
+    (himuon_ns5_ex dispatch): with family "block128" the 128-blocks
+    everywhere; with "auto", LDS-resident for mp == 128 and np <= 256,
     streamed 256-blocks for edges that are multiples of 256, else 128-blocks."""
-    if ns_path() == "small":
+    if family == "block128":
         return "small"
     if mp == 128 and np_ in (128, 256):
         return "lds"

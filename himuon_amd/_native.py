@@ -119,6 +119,14 @@ _SIGNATURES = {
             c_void_p,
         ],
     ),
+    "himuon_ns5_ex": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_float, c_float, c_float, c_void_p,
+         c_size_t, c_int64, c_int, c_void_p],
+    ),
+    "himuon_xxt": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_void_p]),
+    "himuon_ba_plus_caa": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_float, c_float, c_int, c_void_p]),
+    "himuon_bmm_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_int, c_void_p]),
     "himuon_untile": (
         c_int,
         [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p],
@@ -224,10 +232,16 @@ def ns5_workspace_bytes(sub_batch: int, mp: int, np_: int) -> int:
     return int(load().himuon_ns5_workspace_bytes(sub_batch, mp, np_))
 
 
-def ns_path() -> str:
-    """NS kernel family for 256-aligned tiles: HIMUON_NS_PATH = "stream"
-    (persistent streamed-operand kernels, the default) or "small" (128-blocks)."""
-    return os.environ.get("HIMUON_NS_PATH", "stream")
+# himuon_ns5_ex flags (include/himuon_hip.h). Kernel families: AUTO picks per
+# geometry; BLOCK128 runs the 128x128-block kernels everywhere (comparison
+# runs). ROUND_ONCE: the reference's 2-D third product, bf16(B X + a X).
+NS_FAMILY_AUTO = 0
+NS_FAMILY_BLOCK128 = 1
+NS_ROUND_ONCE = 0x10
+NS_FAMILIES = {"auto": NS_FAMILY_AUTO, "block128": NS_FAMILY_BLOCK128}
+# Family every ns5() call runs unless it names one: "auto". Tests and
+# benchmarks that compare families set this attribute; the optimizer never does.
+ns_family_override = "auto"
 
 
 def default_sub_batch(n_tiles: int, mp: int, np_: int) -> int:
@@ -280,31 +294,42 @@ def tile_scale(partials, per_tile, n_tiles, inv, eps=NS_EPS):
     )
 
 
-def ns5(x, y, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, NS_B, NS_C)):
+def ns5(x, y, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, NS_B, NS_C), family=None,
+        round_once=False):
     """NS5 on tiles x; X ping-pongs into y: the result is in x for an even
-    step count and in y for an odd one."""
+    step count and in y for an odd one. ``family`` (a key of NS_FAMILIES)
+    defaults to ``ns_family_override``; ``round_once`` selects the 2-D
+    rounding of the third product."""
     a, b, c = coeffs
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    flags = NS_FAMILIES[family or ns_family_override] | (NS_ROUND_ONCE if round_once else 0)
     _check(
-        load().himuon_ns5(
-            x.data_ptr(),
-            y.data_ptr(),
-            inv.data_ptr(),
-            n_tiles,
-            mp,
-            np_,
-            steps,
-            a,
-            b,
-            c,
-            ws_ptr,
-            ws_bytes,
-            sub_batch,
-            _stream(),
+        load().himuon_ns5_ex(
+            x.data_ptr(), y.data_ptr(), inv.data_ptr(), n_tiles, mp, np_, steps, a, b, c,
+            ws_ptr, ws_bytes, sub_batch, flags, _stream(),
         ),
         "himuon_ns5",
     )
+
+
+def _stage_flags(family, round_once=False) -> int:
+    return NS_FAMILIES[family or ns_family_override] | (NS_ROUND_ONCE if round_once else 0)
+
+
+def xxt(x, out, batch, M, K, family=None):
+    _check(load().himuon_xxt(x.data_ptr(), out.data_ptr(), batch, M, K, _stage_flags(family), _stream()),
+           "himuon_xxt")
+
+
+def ba_plus_caa(a, out, batch, M, alpha, beta, family=None):
+    _check(load().himuon_ba_plus_caa(a.data_ptr(), out.data_ptr(), batch, M, alpha, beta, _stage_flags(family),
+                                     _stream()), "himuon_ba_plus_caa")
+
+
+def bmm_add(b, x, out, batch, M, N, a, round_once=False, family=None):
+    _check(load().himuon_bmm_add(b.data_ptr(), x.data_ptr(), out.data_ptr(), batch, M, N, a,
+                                 _stage_flags(family, round_once), _stream()), "himuon_bmm_add")
 
 
 def untile(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtype, tiles):

@@ -19,7 +19,6 @@
 // LDS with register prefetch of the next K slab. Blocks are mapped to XCDs so
 // all blocks of one NS tile share an L2.
 #include <algorithm>
-#include <cstdlib>
 
 #include "ns5_kernels.h"
 
@@ -160,7 +159,7 @@ __global__ __launch_bounds__(kThreads, 2) void ns_gram_kernel(
 __global__ __launch_bounds__(kThreads, 2) void ns_apply_kernel(
     const uint16_t* __restrict__ Bm, int64_t b_bs, const uint16_t* __restrict__ X, int64_t x_bs,
     uint16_t* __restrict__ Y, int64_t y_bs, const float* __restrict__ inv, int M, int N,
-    int64_t ntiles, float a) {
+    int64_t ntiles, float a, int round_once) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * kLd];
   __shared__ __attribute__((aligned(16))) uint16_t sX[2][(BK / 8) * BN * 8];
 
@@ -263,7 +262,7 @@ __global__ __launch_bounds__(kThreads, 2) void ns_apply_kernel(
         const int j = bj * BN + wn * 64 + ni * 32 + (lane & 31);
         float xv = bf16_to_f32(Xt[(int64_t)i * N + j]);
         if (scaled) xv = round_bf16(xv * sc);
-        const float bx = round_bf16(acc[mi][ni][r]);
+        const float bx = round_once ? acc[mi][ni][r] : round_bf16(acc[mi][ni][r]);
         Yt[(int64_t)i * N + j] = (uint16_t)f32_to_bf16(fmaf(a, xv, bx));
       }
 }
@@ -289,11 +288,15 @@ extern "C" size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np) 
   return 2 * (size_t)sub_batch * mp * mp * sizeof(uint16_t);  // A and B per sub-batch tile
 }
 
-extern "C" int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp,
-                          int np, int steps, float a, float b, float c, void* workspace,
-                          size_t workspace_bytes, int64_t sub_batch, void* stream) {
+extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp,
+                             int np, int steps, float a, float b, float c, void* workspace,
+                             size_t workspace_bytes, int64_t sub_batch, int flags, void* stream) {
+  const int family = flags & HIMUON_NS_FAMILY_MASK;
+  const bool round_once = (flags & HIMUON_NS_ROUND_ONCE) != 0;
   if (!x || !y || x == y || !inv || n_tiles < 0 || steps < 0 || mp <= 0 || np <= 0 || mp > np ||
-      mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN || sub_batch <= 0)
+      mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN || sub_batch <= 0 ||
+      (flags & ~(HIMUON_NS_FAMILY_MASK | HIMUON_NS_ROUND_ONCE)) ||
+      (family != HIMUON_NS_FAMILY_AUTO && family != HIMUON_NS_FAMILY_BLOCK128))
     return HIMUON_EINVAL;
   if (n_tiles == 0) return 0;
   const int64_t sb = sub_batch < n_tiles ? sub_batch : n_tiles;
@@ -312,13 +315,12 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_
 
   uint16_t* wsA = static_cast<uint16_t*>(workspace);
   uint16_t* wsB = wsA + sb * sq;
-  // Tiles whose padded edges are multiples of 256 run the persistent
-  // streamed-operand kernels (ns5_stream.hip); tiles with mp == 128 and
-  // np <= 256 run the fused LDS-resident kernel (ns5_lds.hip);
-  // HIMUON_NS_PATH=small selects the 128-block kernels below for both
-  // (comparison runs). Other tiles always run the 128-block kernels.
-  const char* path = getenv("HIMUON_NS_PATH");
-  const bool small = path && path[0] == 's' && path[1] == 'm';
+  // Family AUTO: tiles whose padded edges are multiples of 256 run the
+  // persistent streamed-operand kernels (ns5_stream.hip); tiles with mp == 128
+  // and np <= 256 run the fused LDS-resident kernel (ns5_lds.hip); other tiles
+  // run the 128-block kernels below, which family BLOCK128 selects for every
+  // geometry.
+  const bool small = family == HIMUON_NS_FAMILY_BLOCK128;
   const bool st = ns5_stream_supported(mp, np) && !small;
   const bool lds = ns5_lds_supported(mp, np) && !small;
   const int nb = mp / BM;
@@ -329,9 +331,9 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_
     const int64_t cnt = std::min<int64_t>(sb, n_tiles - s0);
     const int64_t o = s0 * rect;
     if (lds) {
-      ns5_lds_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, s);
+      ns5_lds_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, s);
     } else if (st) {
-      ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, wsA, wsB, s);
+      ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, wsA, wsB, s);
     } else {
       const uint16_t* cur = x + o;
       uint16_t* nxt = y + o;
@@ -345,7 +347,7 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_
                            c, b);
         hipLaunchKernelGGL(ns_apply_kernel, dim3((unsigned)xcd_grid(cnt * apply_blocks)),
                            dim3(kThreads), 0, s, wsB, sq, cur, rect, nxt, rect, cur_inv, mp, np,
-                           cnt, a);
+                           cnt, a, round_once ? 1 : 0);
         const uint16_t* t = cur;
         cur = nxt;
         nxt = const_cast<uint16_t*>(t);
@@ -356,4 +358,80 @@ extern "C" int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_
     if (e != hipSuccess) return (int)e;
   }
   return 0;
+}
+
+extern "C" int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp,
+                          int np, int steps, float a, float b, float c, void* workspace,
+                          size_t workspace_bytes, int64_t sub_batch, void* stream) {
+  return himuon_ns5_ex(x, y, inv, n_tiles, mp, np, steps, a, b, c, workspace, workspace_bytes,
+                       sub_batch, HIMUON_NS_FAMILY_AUTO, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The three NS products one at a time (the reference's kernel entry points
+// XXT, ba_plus_cAA and fused_bmm_add): contiguous batches, dimensions
+// multiples of 128; edges that are multiples of 256 take the stream kernels
+// (unless the flags ask for the 128-block family), others the 128-block ones.
+// ---------------------------------------------------------------------------
+namespace {
+bool stage_family(int flags, int* family) {
+  *family = flags & HIMUON_NS_FAMILY_MASK;
+  return !(flags & ~HIMUON_NS_FAMILY_MASK) &&
+         (*family == HIMUON_NS_FAMILY_AUTO || *family == HIMUON_NS_FAMILY_BLOCK128);
+}
+}  // namespace
+
+extern "C" int himuon_xxt(const uint16_t* x, uint16_t* out, int64_t batch, int M, int K, int flags,
+                          void* stream) {
+  int family = 0;
+  if (!x || !out || batch < 0 || M <= 0 || K <= 0 || M % BM || K % BM || !stage_family(flags, &family))
+    return HIMUON_EINVAL;
+  if (batch == 0) return 0;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t xs = (int64_t)M * K, os = (int64_t)M * M;
+  if (family == HIMUON_NS_FAMILY_AUTO && M % 256 == 0 && K % 256 == 0) {
+    ns_stream_product(0, x, xs, K, x, xs, K, nullptr, 0, 0, out, os, M, M, M, K, batch, 1.f, 0.f, false, s);
+  } else {
+    const int nb = M / BM;
+    hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(batch * (nb * (nb + 1) / 2))), dim3(kThreads), 0,
+                       s, x, xs, K, out, os, M, nullptr, M, K, batch, 1.0f, 0.0f);
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int himuon_ba_plus_caa(const uint16_t* a, uint16_t* out, int64_t batch, int M, float alpha,
+                                  float beta, int flags, void* stream) {
+  int family = 0;
+  if (!a || !out || a == out || batch < 0 || M <= 0 || M % BM || !stage_family(flags, &family))
+    return HIMUON_EINVAL;
+  if (batch == 0) return 0;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t sq = (int64_t)M * M;
+  if (family == HIMUON_NS_FAMILY_AUTO && M % 256 == 0) {
+    ns_stream_product(1, a, sq, M, a, sq, M, a, sq, M, out, sq, M, M, M, M, batch, alpha, beta, false, s);
+  } else {
+    const int nb = M / BM;
+    hipLaunchKernelGGL(ns_gram_kernel, dim3((unsigned)xcd_grid(batch * (nb * (nb + 1) / 2))), dim3(kThreads), 0,
+                       s, a, sq, M, out, sq, M, nullptr, M, M, batch, alpha, beta);
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int himuon_bmm_add(const uint16_t* b, const uint16_t* x, uint16_t* out, int64_t batch, int M, int N,
+                              float a, int flags, void* stream) {
+  int family = 0;
+  const bool round_once = (flags & HIMUON_NS_ROUND_ONCE) != 0;
+  if (!b || !x || !out || out == x || out == b || batch < 0 || M <= 0 || N <= 0 || M % BM || N % BN ||
+      !stage_family(flags & ~HIMUON_NS_ROUND_ONCE, &family))
+    return HIMUON_EINVAL;
+  if (batch == 0) return 0;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t sq = (int64_t)M * M, rect = (int64_t)M * N;
+  if (family == HIMUON_NS_FAMILY_AUTO && M % 256 == 0 && N % 256 == 0) {
+    ns_stream_product(2, b, sq, M, x, rect, N, x, rect, N, out, rect, N, M, N, M, batch, 1.f, a, round_once, s);
+  } else {
+    hipLaunchKernelGGL(ns_apply_kernel, dim3((unsigned)xcd_grid(batch * (M / BM) * (N / BN))), dim3(kThreads), 0,
+                       s, b, sq, x, rect, out, rect, nullptr, M, N, batch, a, round_once ? 1 : 0);
+  }
+  return (int)hipGetLastError();
 }

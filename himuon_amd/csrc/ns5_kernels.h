@@ -103,14 +103,27 @@ HM_DEV u32x2_t quad_transpose(u32x2_t w, int k) {
 
 // Persistent streamed-operand 256-block path (ns5_stream.hip): mp, np
 // multiples of 256. Scales x in place (X0), then runs `steps` iterations on
-// `cnt` tiles, ping-ponging X between x and y.
+// `cnt` tiles, ping-ponging X between x and y. round_once: the third product
+// rounds bf16(B X + a X) once (the 2-D form) instead of bf16(bf16(B X) + a X).
 bool ns5_stream_supported(int mp, int np);
 void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
-                    float a, float b, float c, uint16_t* wsA, uint16_t* wsB, hipStream_t s);
+                    float a, float b, float c, bool round_once, uint16_t* wsA, uint16_t* wsB,
+                    hipStream_t s);
+
+// One NS product over `ntiles` batch entries on the 256-block stream kernels
+// (M, N, K multiples of 256; row pitches in elements, batch strides):
+//   mode 0: C = bf16(P P^T)                      P: M x K, C: M x M
+//   mode 1: C = bf16(alpha P P^T + beta R)       R = P, K = M
+//   mode 2: C = bf16(bf16(P Q) + beta R)         P: M x K (K = M), Q, R, C: M x N
+//           (bf16(P Q + beta R) with round_once)
+void ns_stream_product(int mode, const uint16_t* P, int64_t p_bs, int ldp, const uint16_t* Q, int64_t q_bs,
+                       int ldq, const uint16_t* R, int64_t r_bs, int ldr, uint16_t* C, int64_t c_bs, int ldc,
+                       int M, int N, int K, int64_t ntiles, float alpha, float beta, bool round_once,
+                       hipStream_t s);
 
 // Fused LDS-resident path (ns5_lds.hip): mp == 128, np = 128 or 256. Runs
 // `steps` >= 1 iterations of `cnt` tiles in one launch; reads X from x and
 // leaves the result in x (even `steps`) or y (odd), as the other paths do.
 bool ns5_lds_supported(int mp, int np);
 void ns5_lds_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
-                 float a, float b, float c, hipStream_t s);
+                 float a, float b, float c, bool round_once, hipStream_t s);

@@ -161,11 +161,11 @@ HM_DEV void gram_b(const lds_u8* A, int lane, float cb, float cc, u32x2_t (&o)[3
 }
 
 template <int NQ>
-__global__ __launch_bounds__(NT, NQ == 1 ? 2 : 1) void ns5_lds_kernel(const uint16_t* __restrict__ x,
-                                                        uint16_t* __restrict__ out,
+__global__ __launch_bounds__(NT, NQ == 1 ? 2 : 1) void ns5_lds_kernel(const uint16_t* x,
+                                                        uint16_t* out,
                                                         const float* __restrict__ inv,
                                                         int64_t ntiles, int steps, float ca,
-                                                        float cb, float cc) {
+                                                        float cb, float cc, int round_once) {
   constexpr int N = 128 * NQ;   // NS columns (np)
   constexpr int XCH = N / 8;    // 16-byte chunks per X row
   constexpr int ACH = M / 8;    // chunks per A row
@@ -280,7 +280,8 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 2 : 1) void ns5_lds_kernel(const uint
               float y[4];
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
-                const float bx = bf16_to_f32(pk_bf16(acc[tj][ti][4 * q + e], 0.f) & 0xffffu);
+                const float v = acc[tj][ti][4 * q + e];
+                const float bx = round_once ? v : bf16_to_f32(pk_bf16(v, 0.f) & 0xffffu);
                 y[e] = fmaf(ca, bf16_to_f32(half16(rv[e >> 1], e & 1)), bx);
               }
               o[ti][tj][q] = u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
@@ -324,12 +325,12 @@ int num_cus() {
 bool ns5_lds_supported(int mp, int np) { return mp == M && (np == 128 || np == 256); }
 
 void ns5_lds_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
-                 float a, float b, float c, hipStream_t s) {
+                 float a, float b, float c, bool round_once, hipStream_t s) {
   (void)mp;
   uint16_t* out = (steps & 1) ? y : x;
   const int64_t wgs = std::min<int64_t>(cnt, (int64_t)(np == 128 ? 2 : 1) * 4 * num_cus());
   if (np == 128)
-    hipLaunchKernelGGL(ns5_lds_kernel<1>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c);
+    hipLaunchKernelGGL(ns5_lds_kernel<1>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
   else
-    hipLaunchKernelGGL(ns5_lds_kernel<2>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c);
+    hipLaunchKernelGGL(ns5_lds_kernel<2>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
 }

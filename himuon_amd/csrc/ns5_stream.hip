@@ -58,6 +58,7 @@ struct StArgs {
   int M, N, K;
   int64_t ntiles;
   float alpha, beta;                           // GramB: c, b; Apply: beta = a
+  int round_once;                              // Apply: bf16(B X + a X), one rounding
 };
 
 // Workgroup barrier for LDS reuse: this wave's LDS operations are complete;
@@ -386,8 +387,8 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
           for (int e = 0; e < 4; ++e) {
             const float x = bf16_to_f32(half16(rv[e >> 1], e & 1));
             const float v = acc[tj][ti][4 * q + e];
-            if constexpr (MODE == kApply)
-              y[e] = fmaf(g.beta, x, bf16_to_f32(pk_bf16(v, 0.f) & 0xffffu));  // bf16(B X) + a X
+            if constexpr (MODE == kApply)  // bf16(B X) + a X, or B X + a X (2-D form)
+              y[e] = fmaf(g.beta, x, g.round_once ? v : bf16_to_f32(pk_bf16(v, 0.f) & 0xffffu));
             else
               y[e] = fmaf(g.beta, x, g.alpha * v);  // c (A A^T) + b A
           }
@@ -540,19 +541,14 @@ __global__ __launch_bounds__(NT) void ns_st_scale_kernel(uint16_t* __restrict__ 
   }
 }
 
-int g_num_cus[16] = {0};
-
+// CUs of the current device, queried per launch (a host-side attribute
+// lookup; nothing is cached in the library).
 int num_cus() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
-  const int d = dev & 15;
-  if (g_num_cus[d] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    g_num_cus[d] = n;
-  }
-  return g_num_cus[d];
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  return n;
 }
 
 template <int MODE>
@@ -573,11 +569,27 @@ void launch(const StArgs& a, int64_t items, hipStream_t s) {
 
 bool ns5_stream_supported(int mp, int np) { return mp % BT == 0 && np % BT == 0; }
 
+void ns_stream_product(int mode, const uint16_t* P, int64_t p_bs, int ldp, const uint16_t* Q, int64_t q_bs,
+                       int ldq, const uint16_t* R, int64_t r_bs, int ldr, uint16_t* C, int64_t c_bs, int ldc,
+                       int M, int N, int K, int64_t ntiles, float alpha, float beta, bool round_once,
+                       hipStream_t s) {
+  const StArgs g{P, p_bs, ldp, Q, q_bs, ldq, R, r_bs, ldr, C, c_bs, ldc, M, N, K, ntiles, alpha, beta,
+                 round_once ? 1 : 0};
+  const int nb = M / BT;
+  if (mode == kApply)
+    launch<kApply>(g, ntiles * nb * (N / BT), s);
+  else if (mode == kGramB)
+    launch<kGramB>(g, ntiles * (nb * (nb + 1) / 2), s);
+  else
+    launch<kGramA>(g, ntiles * (nb * (nb + 1) / 2), s);
+}
+
 // One sub-batch of `cnt` tiles, `steps` >= 1 iterations, ping-ponging X
 // between x and y (x is scaled in place first); A and B live in the
 // workspace.
 void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
-                    float a, float b, float c, uint16_t* wsA, uint16_t* wsB, hipStream_t s) {
+                    float a, float b, float c, bool round_once, uint16_t* wsA, uint16_t* wsB,
+                    hipStream_t s) {
   const int64_t sq = (int64_t)mp * mp, rect = (int64_t)mp * np;
   const int nb = mp / BT;
   const int64_t gram_items = cnt * (nb * (nb + 1) / 2);
@@ -588,11 +600,11 @@ void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int
   uint16_t* cur = x;
   uint16_t* nxt = y;
   for (int it = 0; it < steps; ++it) {
-    const StArgs ga{cur, rect, np, cur, rect, np, nullptr, 0, 0, wsA, sq, mp, mp, mp, np, cnt, 1.0f, 0.0f};
+    const StArgs ga{cur, rect, np, cur, rect, np, nullptr, 0, 0, wsA, sq, mp, mp, mp, np, cnt, 1.0f, 0.0f, 0};
     launch<kGramA>(ga, gram_items, s);
-    const StArgs gb{wsA, sq, mp, wsA, sq, mp, wsA, sq, mp, wsB, sq, mp, mp, mp, mp, cnt, c, b};
+    const StArgs gb{wsA, sq, mp, wsA, sq, mp, wsA, sq, mp, wsB, sq, mp, mp, mp, mp, cnt, c, b, 0};
     launch<kGramB>(gb, gram_items, s);
-    const StArgs ap{wsB, sq, mp, cur, rect, np, cur, rect, np, nxt, rect, np, mp, np, mp, cnt, 1.0f, a};
+    const StArgs ap{wsB, sq, mp, cur, rect, np, cur, rect, np, nxt, rect, np, mp, np, mp, cnt, 1.0f, a, round_once ? 1 : 0};
     launch<kApply>(ap, apply_items, s);
     std::swap(cur, nxt);
   }

@@ -51,8 +51,12 @@ class TileGroup:
         dtype: torch.dtype,
         upd_dtype: torch.dtype | None = None,
         apply_groups: list[int] | None = None,
+        round_once: bool = False,
     ):
         self.tile_h, self.tile_w = int(tile_h), int(tile_w)
+        # NS third product rounded once (the reference's 2-D addmm form,
+        # himuon.py:249-253): full-matrix groups and 2-D newton_schulz calls.
+        self.round_once = bool(round_once)
         self.m, self.n, self.mp, self.np, self.trans = nat.ns_geometry(self.tile_h, self.tile_w)
         self.device = device
         self.dtype = dtype  # grads and momentum
@@ -157,7 +161,7 @@ class TileGroup:
         nat.ns5(
             r(self.tiles, start, count), r(self.alt, start, count),
             self.inv[start : start + count], count, self.mp, self.np, steps,
-            workspace, sub_batch,
+            workspace, sub_batch, round_once=self.round_once,
         )
 
     def result(self, steps: int) -> torch.Tensor:
@@ -274,7 +278,9 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
 
     The batch is viewed as one (B*M, N) matrix cut into M x N tiles, so the
     gather/untile kernels handle the cast, the transpose-if-tall and the
-    padding (himuon.py:263-284, test_kernels.py:176-198)."""
+    padding (himuon.py:263-284, test_kernels.py:176-198). A 2-D ``G`` takes
+    the reference's 2-D rounding of the third product (torch.addmm,
+    himuon.py:249-253); a batched one that of fused_bmm_add."""
     assert G.ndim >= 2
     if not G.is_cuda:
         raise RuntimeError("HiMuon.newton_schulz runs on the HIP device only (no CPU path)")
@@ -292,6 +298,7 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
         nesterovs=[False],
         device=G.device,
         dtype=dtype,
+        round_once=G.ndim == 2,
     )
     out = grp.updates[0]
     sb = grp.default_sub_batch()

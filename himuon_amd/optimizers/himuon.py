@@ -120,6 +120,9 @@ class HiMuon(Optimizer):
         # Device state of the HIP path, rebuilt after reconfigure().
         self._groups: "list[dict] | None" = None  # tiled buckets + full-NS shape groups
         self._workspace: "torch.Tensor | None" = None
+        # (param, param storage, grad storage) of every parameter with a grad
+        # when the device state (plan, descriptor tables, graph) was built.
+        self._state_sig: "tuple | None" = None
 
         if lr_adjust not in ("none", "tile"):
             raise ValueError(f"lr_adjust must be 'none' or 'tile', got {lr_adjust!r}")
@@ -168,6 +171,31 @@ class HiMuon(Optimizer):
         self._apply_tables = None
         self._adamw_tables = None
         self._adamw_sig = None
+
+    def _storage_sig(self) -> tuple:
+        """Which parameters have a grad, and where each such parameter's and
+        grad's storage lives. The plan, the device descriptor tables and a
+        captured graph all hold these pointers."""
+        return tuple(
+            (id(p), p.data_ptr(), p.grad.data_ptr())
+            for g in self.param_groups
+            for p in g["params"]
+            if p.grad is not None
+        )
+
+    def _check_storage(self) -> None:
+        """Drop the plan, device state and graph when the set of parameters
+        with grads, or the storage of any of them or of its grad, changed since
+        they were built (the next steps warm up and recapture, as after
+        reconfigure; momentum and AdamW state are kept). The reference scans
+        the full-matrix parameters every step and skips those without a grad
+        (himuon.py:846-858) and reads p.data at every update
+        (himuon.py:222-228, 343-348)."""
+        sig = self._storage_sig()
+        if sig != self._state_sig:
+            if self._state_sig is not None:
+                self._invalidate_plan_cache()
+            self._state_sig = sig
 
     def _scale_alpha(self) -> list[float]:
         """(1 - lr*wd, -lr) per param group: the two factors of p.mul_(1 - lr*wd);
@@ -528,6 +556,9 @@ class HiMuon(Optimizer):
                 dtype=dtype,
                 upd_dtype=update_dtype(params, dtype),
                 apply_groups=gidx if fusable(params, gidx, dtype) else None,
+                # the reference calls newton_schulz on the 2-D momentum
+                # (himuon.py:861), whose third product is torch.addmm (249-253)
+                round_once=True,
             )
             out.append(
                 {
@@ -670,6 +701,7 @@ class HiMuon(Optimizer):
         if closure is not None:
             loss = closure()
         self._check_device()
+        self._check_storage()
         dev = next((p.grad.device for g in self.param_groups for p in g["params"] if p.grad is not None), None)
         if dev is not None and dev.type == "cuda":
             self._write_lrwd(dev)

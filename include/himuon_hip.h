@@ -148,6 +148,51 @@ int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles,
                void* stream);
 
 /*
+ * himuon_ns5 with option flags (himuon_ns5 is flags == 0):
+ *  - HIMUON_NS_ROUND_ONCE: the third product of every iteration is rounded
+ *    once, X = bf16(B X + a X) (fp32 B X), as the reference's 2-D path
+ *    torch.addmm(X, B, X, beta=a) computes it (himuon.py:249-253; its
+ *    batched 3-D path, fused_bmm_add, rounds B X first). The optimizer sets
+ *    it for full-matrix parameters and 2-D newton_schulz calls.
+ *  - kernel family (bits HIMUON_NS_FAMILY_MASK; no reference counterpart,
+ *    for comparison tests and benchmarks): HIMUON_NS_FAMILY_AUTO picks per
+ *    geometry as himuon_ns5 does; HIMUON_NS_FAMILY_BLOCK128 runs the
+ *    128x128-block kernels for every geometry. Results are identical.
+ * Any other flag bit is an argument error.
+ */
+#define HIMUON_NS_FAMILY_MASK 0x0F
+#define HIMUON_NS_FAMILY_AUTO 0
+#define HIMUON_NS_FAMILY_BLOCK128 1
+#define HIMUON_NS_ROUND_ONCE 0x10
+int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles,
+                  int mp, int np, int steps, float a, float b, float c,
+                  void* workspace, size_t workspace_bytes, int64_t sub_batch,
+                  int flags, void* stream);
+
+/*
+ * The three NS products one at a time, on contiguous bf16 batches (no
+ * normaliser, one product per call). They replace the reference's kernel entry
+ * points XXT(A, out) (triton_kernels/XXT.py:76-104), ba_plus_cAA(A, alpha,
+ * beta, out) (ba_plus_cAA.py:90-120) and fused_bmm_add(B, X, a, out)
+ * (fused_bmm_add.py:98-135) with the same rounding points as himuon_ns5:
+ *   himuon_xxt:         out = bf16(x x^T)            x: (batch, M, K), out: (batch, M, M)
+ *   himuon_ba_plus_caa: out = bf16(alpha a a^T + beta a)   a, out: (batch, M, M)
+ *   himuon_bmm_add:     out = bf16(bf16(b x) + a x)   b: (batch, M, M), x, out: (batch, M, N)
+ *                       (bf16(b x + a x), one rounding, with HIMUON_NS_ROUND_ONCE:
+ *                       torch.addmm(X, B, X, beta=a) of himuon.py:252-253)
+ * M, N, K multiples of HIMUON_NS_ALIGN (pad with zeros: zero rows and columns
+ * are exact). `flags` takes a kernel family (HIMUON_NS_FAMILY_*) and, for
+ * himuon_bmm_add, HIMUON_NS_ROUND_ONCE. Outputs must not alias inputs. The
+ * Gram outputs are exactly symmetric.
+ */
+int himuon_xxt(const uint16_t* x, uint16_t* out, int64_t batch, int M, int K,
+               int flags, void* stream);
+int himuon_ba_plus_caa(const uint16_t* a, uint16_t* out, int64_t batch, int M,
+                       float alpha, float beta, int flags, void* stream);
+int himuon_bmm_add(const uint16_t* b, const uint16_t* x, uint16_t* out,
+                   int64_t batch, int M, int N, float a, int flags, void* stream);
+
+/*
  * Untile/scatter: for every element of every parameter,
  *     update[row, col] = round_dtype(upd_scale * float(NS tile value))
  * reading the NS tile position of (row, col) (transposed back when

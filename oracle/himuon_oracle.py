@@ -20,10 +20,18 @@ Functions and the reference lines they restate:
                         test_kernels.py:176-198 with exact arithmetic)
   ns5_spectral          the same map through an SVD (closed form used to pin
                         ns5_fp64)
+  xxt / ba_plus_caa / bmm_add / ns_iteration
+                        the three products of one NS iteration at the
+                        reference kernels' rounding points (XXT.py:55-75,
+                        ba_plus_cAA.py:58-85, fused_bmm_add.py:73-88; the
+                        2-D third product torch.addmm, himuon.py:249-253)
   ns5_staged            NS with the rounding points of the HIP kernels and the
                         reference kernels: bf16 after every GEMM stage, fp32
                         accumulation (ns5_smem.py:84-101, XXT.py:62-70,
                         ba_plus_cAA.py:78-85, fused_bmm_add.py:73-88)
+  ns5_staged_2d         ns5_staged with the 2-D third product of
+                        himuon.py:249-253 (torch.addmm: bf16(B X + a X),
+                        one rounding)
   ns5_eager             NS with the rounding of the eager-torch oracle of
                         tests/integration/test_kernels.py:176-198 (every torch
                         op rounds to bf16)
@@ -293,14 +301,47 @@ def _mm32(x: np.ndarray, y: np.ndarray) -> np.ndarray:
     return np.matmul(x.astype(F32), y.astype(F32))
 
 
-def ns5_staged(G, steps: int = 5, coeffs=(NS_A, NS_B, NS_C), eps: float = NS_EPS) -> np.ndarray:
+def xxt(X) -> np.ndarray:
+    """A = bf16(X X^T), fp32 accumulation (XXT.py:55-75)."""
+    return bf16_round(_mm32(X, np.swapaxes(X, -1, -2)))
+
+
+def ba_plus_caa(A, alpha: float, beta: float) -> np.ndarray:
+    """B = bf16(alpha * (A A^T) + beta * A), fp32 accumulation and epilogue
+    (ba_plus_cAA.py:58-85)."""
+    return bf16_round(F32(alpha) * _mm32(A, np.swapaxes(A, -1, -2)) + F32(beta) * np.asarray(A, F32))
+
+
+def bmm_add(B, X, a: float, round_once: bool = False) -> np.ndarray:
+    """X' = bf16(bf16(B X) + a X) (fused_bmm_add.py:73-88, the batched form),
+    or with round_once bf16(B X + a X) from the fp32 product, one rounding
+    (torch.addmm(X, B, X, beta=a), the 2-D form of himuon.py:249-253)."""
+    X = np.asarray(X, F32)
+    if round_once:
+        return bf16_round(fma32(F32(a), X, _mm32(B, X)))
+    return bf16_round(bf16_round(_mm32(B, X)) + F32(a) * X)
+
+
+def ns_iteration(X, coeffs=(NS_A, NS_B, NS_C), round_once: bool = False):
+    """One NS iteration at the kernels' rounding points: (A, B, X')."""
+    a, b, c = coeffs
+    A = xxt(X)
+    B = ba_plus_caa(A, c, b)
+    return A, B, bmm_add(B, X, a, round_once)
+
+
+def ns5_staged(G, steps: int = 5, coeffs=(NS_A, NS_B, NS_C), eps: float = NS_EPS,
+               round_once: bool = False) -> np.ndarray:
     """NS with the kernel rounding points; (..., M, N) float32 -> float32
     holding bf16 values.
 
         X0 = bf16(x * (1 / (||x||_F + eps)))     x = bf16(G), norm in fp32
         A  = bf16(X X^T)
         B  = bf16(c * (A A^T) + b * A)
-        X  = bf16(bf16(B X) + a * X)
+        X  = bf16(bf16(B X) + a * X)             batched (3-D) form, fused_bmm_add
+        X  = bf16(B X + a * X)                   round_once: the 2-D form,
+                                                 torch.addmm(X, B, X, beta=a)
+                                                 (himuon.py:249-253)
     """
     a, b, c = (F32(v) for v in coeffs)
     X = bf16_round(np.asarray(G, dtype=F32))
@@ -311,12 +352,18 @@ def ns5_staged(G, steps: int = 5, coeffs=(NS_A, NS_B, NS_C), eps: float = NS_EPS
     inv = (F32(1.0) / (nrm + F32(eps))).astype(F32)
     X = bf16_round(X * inv)
     for _ in range(steps):
-        A = bf16_round(_mm32(X, np.swapaxes(X, -1, -2)))
-        B = bf16_round(c * _mm32(A, np.swapaxes(A, -1, -2)) + b * A)
-        X = bf16_round(bf16_round(_mm32(B, X)) + a * X)
+        _, _, X = ns_iteration(X, coeffs, round_once)
     if tall:
         X = np.ascontiguousarray(np.swapaxes(X, -1, -2))
     return X
+
+
+def ns5_staged_2d(G, steps: int = 5, coeffs=(NS_A, NS_B, NS_C), eps: float = NS_EPS) -> np.ndarray:
+    """ns5_staged with the reference's 2-D third product (one rounding of
+    B X + a X, torch.addmm; himuon.py:249-253): what newton_schulz computes
+    for a 2-D input and the full-matrix path (himuon.py:861) for each
+    parameter. Batched inputs are treated as independent 2-D matrices."""
+    return ns5_staged(G, steps, coeffs, eps, round_once=True)
 
 
 def ns5_eager(G, steps: int = 5, coeffs=(NS_A, NS_B, NS_C), eps: float = NS_EPS) -> np.ndarray:
@@ -448,8 +495,8 @@ def step_param(op: OracleParam, ns=ns5_staged):
     ge, nb = momentum(op.g, buf, op.mu, op.nesterov, op.g_dtype)
     h, w = ge.shape
     th, tw = op.tile
-    if h * w <= th * tw:  # full-NS path (himuon.py:852-874)
-        u = ns(ge, op.ns_steps)
+    if h * w <= th * tw:  # full-NS path (himuon.py:852-874): a 2-D NS call
+        u = ns(ge, op.ns_steps, round_once=True) if ns is ns5_staged else ns(ge, op.ns_steps)
         scale = lr_scale((h, w), op.lr_adjust)
     else:
         tiles = tile(ge, th, tw)

@@ -28,7 +28,10 @@ def _t(x):
     return x.transpose(-2, -1).contiguous()
 
 
-def ns5_torch_staged(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
+def ns5_torch_staged(G: torch.Tensor, steps: int = 5, round_once: bool = False) -> torch.Tensor:
+    """round_once: the reference's 2-D third product, torch.addmm(X, B, X,
+    beta=a) per matrix (himuon.py:249-253), instead of the batched
+    fused_bmm_add form."""
     shape, dtype = G.shape, G.dtype
     X = G.reshape(-1, shape[-2], shape[-1]).to(torch.bfloat16)
     tall = shape[-2] > shape[-1]
@@ -40,8 +43,11 @@ def ns5_torch_staged(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     for _ in range(steps):
         Am = _bmm(X, _t(X))  # bf16 out, fp32 accumulate
         Bm = torch.baddbmm(Am, Am, _t(Am), beta=B, alpha=C)  # fp32 epilogue, one rounding
-        BX = _bmm(Bm, X)
-        X = torch.add(BX, X, alpha=A)  # bf16(float(BX) + a * float(X))
+        if round_once:
+            X = torch.stack([torch.addmm(X[i], Bm[i], X[i], beta=A, alpha=1.0) for i in range(X.shape[0])])
+        else:
+            BX = _bmm(Bm, X)
+            X = torch.add(BX, X, alpha=A)  # bf16(float(BX) + a * float(X))
     if tall:
         X = _t(X)
     return X.reshape(shape).to(dtype)

@@ -14,8 +14,7 @@ sys.path.insert(0, ROOT)
 import bench  # noqa: E402
 
 
-def test_ns_family_follows_the_library_dispatch(monkeypatch):
-    monkeypatch.delenv("HIMUON_NS_PATH", raising=False)
+def test_ns_family_follows_the_library_dispatch():
     # LDS-resident kernel: mp == 128 and np <= 256
     assert bench.ns_family(128, 128) == "lds"
     assert bench.ns_family(128, 256) == "lds"
@@ -27,8 +26,7 @@ def test_ns_family_follows_the_library_dispatch(monkeypatch):
     assert bench.ns_family(128, 384) == "small"
     assert bench.ns_family(640, 768) == "small"
     assert bench.ns_family(384, 384) == "small"
-    monkeypatch.setenv("HIMUON_NS_PATH", "small")
-    assert bench.ns_family(512, 512) == "small"
+    assert bench.ns_family(512, 512, "block128") == "small"
     assert set(bench.NS_KERNELS) == {"stream", "lds", "small"}
 
 

@@ -143,6 +143,25 @@ def test_argument_errors_return_before_launch(lib):
     assert lib.himuon_tile_scale(8, 16, 0, 1e-7, 8, z) == 0
 
 
+def test_ns5_ex_and_stage_argument_errors(lib):
+    z = None
+    # unknown flag bits or family codes
+    assert lib.himuon_ns5_ex(8, 16, 8, 4, 512, 512, 5, 1.0, 1.0, 1.0, 8, 1 << 30, 4, 0x40, z) == -22
+    assert lib.himuon_ns5_ex(8, 16, 8, 4, 512, 512, 5, 1.0, 1.0, 1.0, 8, 1 << 30, 4, 7, z) == -22
+    # the flags that exist are accepted (empty work returns before any launch)
+    assert lib.himuon_ns5_ex(8, 16, 8, 0, 512, 512, 5, 1.0, 1.0, 1.0, 8, 1 << 30, 4, 0x11, z) == 0
+    # stage products: null pointers, unaligned dimensions, aliasing, bad flags
+    assert lib.himuon_xxt(z, 8, 1, 256, 256, 0, z) == -22
+    assert lib.himuon_xxt(8, 16, 1, 200, 256, 0, z) == -22
+    assert lib.himuon_xxt(8, 16, 1, 256, 256, 0x10, z) == -22  # round-once is for bmm_add only
+    assert lib.himuon_ba_plus_caa(8, 8, 1, 256, 1.0, 1.0, 0, z) == -22
+    assert lib.himuon_ba_plus_caa(8, 16, 1, 100, 1.0, 1.0, 0, z) == -22
+    assert lib.himuon_bmm_add(8, 16, 16, 1, 256, 256, 1.0, 0, z) == -22
+    assert lib.himuon_bmm_add(8, 16, 24, 1, 256, 200, 1.0, 0, z) == -22
+    assert lib.himuon_bmm_add(8, 16, 24, 1, 256, 256, 1.0, 0x20, z) == -22
+    assert lib.himuon_bmm_add(8, 16, 24, 0, 256, 256, 1.0, 0x10, z) == 0
+
+
 def test_geometry_helpers():
     assert nat.ns_geometry(512, 512) == (512, 512, 512, 512, False)
     assert nat.ns_geometry(768, 513) == (513, 768, 640, 768, True)

@@ -69,12 +69,12 @@ GATHER_CASES = [
 ]
 
 
-@pytest.fixture(params=["stream", "small"])
+@pytest.fixture(params=["auto", "block128"])
 def ns_family(request, monkeypatch):
-    """Run a test under each NS kernel family (persistent streamed-operand
-    256-blocks, the default, and 128-blocks); shapes the 256-block family
-    cannot take run the 128-block kernels."""
-    monkeypatch.setenv("HIMUON_NS_PATH", request.param)
+    """Run a test under each NS kernel family selection: "auto" (the
+    product's per-geometry choice: LDS-resident, persistent streamed 256-blocks
+    or 128-blocks) and "block128" (the 128-block kernels for every geometry)."""
+    monkeypatch.setattr(nat, "ns_family_override", request.param)
     return request.param
 
 
@@ -182,7 +182,9 @@ def test_newton_schulz_matches_reference_on_well_conditioned(label, shape, ns_fa
     assert torch.isfinite(out).all()
     ref_eager = ns5_torch_eager(G)
     assert torch.allclose(out.float(), ref_eager.float(), rtol=4e-2, atol=4e-2), label
-    ref = ns5_torch_staged(G)
+    # a 2-D input takes the reference's 2-D third product (torch.addmm,
+    # himuon.py:249-253), a batched one fused_bmm_add's
+    ref = ns5_torch_staged(G, round_once=G.ndim == 2)
     err = per_tile_rel_fro(out, ref)
     print(f"  rel-fro vs staged torch: max {err.max():.4f} mean {err.mean():.4f}", flush=True)
     assert err.max() <= 1e-2, err
@@ -203,10 +205,14 @@ def test_ns5_random_tiles_vs_oracle_and_torch(T, n, ns_family):
     floor = per_tile_rel_fro(ref_t, ref_o)
     print(f"  vs torch max {e_t.max():.4f} mean {e_t.mean():.4f} | vs oracle max {e_o.max():.4f} "
           f"mean {e_o.mean():.4f} | torch vs oracle max {floor.max():.4f} mean {floor.mean():.4f}", flush=True)
-    assert e_t.mean() <= 1e-2 and e_o.mean() <= 1e-2
-    assert e_t.max() <= 2e-2 and e_o.max() <= 2e-2
-    # as close to each reference as the two references are to each other
-    assert e_t.mean() <= 1.5 * floor.mean() + 1e-3
+    # the north star's bar against the reference's NS5 in the same dtypes,
+    # and bit-identity as built (same rounding points, same k order)
+    assert e_t.max() <= 1e-2
+    assert torch.equal(out, ref_t.to(out.dtype))
+    # the numpy oracle sums in another order: bf16 NS5 amplifies that to the
+    # noise floor the two references show against each other
+    assert e_o.mean() <= 1e-2 and e_o.max() <= 2e-2
+    assert e_o.mean() <= 1.5 * floor.mean() + 1e-3
 
 
 @pytest.mark.parametrize("T,n", [(128, 16), (512, 4)])
@@ -300,7 +306,7 @@ def test_ns5_ignores_stale_buffer_contents(label, n, M, N, ns_family):
     assert torch.isfinite(outs[1].float()).all()
     assert torch.equal(outs[0], outs[1])
     err = per_tile_rel_fro(outs[1].view(n, M, N).float(), ns5_torch_staged(G).float())
-    assert err.max() <= 2e-2, err
+    assert err.max() <= 1e-2, err
 
 
 def test_ns5_workspace_too_small_raises():
@@ -339,4 +345,5 @@ def test_ns5_many_tiles_large_buffers():
     ref = ns5_torch_staged(G[idx])
     err = per_tile_rel_fro(out[idx].float(), ref.float())
     print(f"  sampled tiles vs staged torch: max {err.max():.4f} mean {err.mean():.4f}", flush=True)
-    assert err.mean() <= 1e-2 and err.max() <= 2e-2
+    assert err.max() <= 1e-2
+    assert torch.equal(out[idx], ref)

@@ -504,3 +504,58 @@ def test_step_param_composes_reference_formula():
     expect = p * (1 - 1e-3) - 1e-2 * 0.2 * 8.0 * u
     assert _rel_fro(newp - p * (1 - 1e-3), expect - p * (1 - 1e-3)) < 3e-2
     assert np.array_equal(nb, g)
+
+
+def test_bmm_add_forms_match_torch_rounding():
+    """The third product's two roundings: torch.addmm (the reference's 2-D
+    path) rounds B X + a X once; fused_bmm_add's form rounds B X first. A
+    crafted 1x1 case separates them: B X = 1 + 2^-9 + ... is a bf16 tie-breaker
+    only with a X added before rounding."""
+    B = np.array([[1.0 + 2**-7]], np.float32)
+    X = np.array([[1.0 - 2**-8]], np.float32)
+    a = 2.0**-12
+    once = O.bmm_add(B, X, a, round_once=True)
+    twice = O.bmm_add(B, X, a)
+    tb, tx = torch.from_numpy(B).bfloat16(), torch.from_numpy(X).bfloat16()
+    ref_once = torch.addmm(tx, tb, tx, beta=a).float().numpy()
+    ref_twice = (torch.mm(tb, tx).float() + a * tx.float()).bfloat16().float().numpy()
+    assert once[0, 0] == 1.0078125 and twice[0, 0] == 1.0
+    assert np.array_equal(once, ref_once) and np.array_equal(twice, ref_twice)
+
+
+def test_ns_iteration_stages_match_torch_ops_on_exact_inputs():
+    """Stage by stage against torch's CPU ops on inputs whose fp32 sums are
+    exact (entries in {-2,...,2} * 2^-4): A = bmm(X, X^T), B = baddbmm(A, A,
+    A^T, beta=b, alpha=c), X' both forms; and the full iteration composes them."""
+    rng = np.random.default_rng(3)
+    X = (rng.integers(-2, 3, size=(2, 16, 24)) * 2.0**-4).astype(np.float32)
+    a, b, c = O.NS_A, O.NS_B, O.NS_C
+    tx = torch.from_numpy(X).bfloat16()
+    A = O.xxt(X)
+    assert np.array_equal(A, torch.bmm(tx, tx.transpose(1, 2).contiguous()).float().numpy())
+    assert np.array_equal(A, np.swapaxes(A, 1, 2))
+    tA = torch.from_numpy(A).bfloat16()
+    Bm = O.ba_plus_caa(A, c, b)
+    # fp32 product (exact here): the bf16 bmm would round A A^T before the epilogue
+    acc = torch.bmm(tA.float(), tA.float().transpose(1, 2).contiguous())
+    ref_B = (c * acc + b * tA.float()).bfloat16()
+    assert np.array_equal(Bm, ref_B.float().numpy())
+    tB = torch.from_numpy(Bm).bfloat16()
+    for i in range(2):
+        got = O.bmm_add(Bm[i], X[i], a, round_once=True)
+        assert np.array_equal(got, torch.addmm(tx[i], tB[i], tx[i], beta=a).float().numpy())
+    got3 = O.bmm_add(Bm, X, a)
+    ref3 = (torch.bmm(tB, tx).float() + a * tx.float()).bfloat16().float().numpy()
+    assert np.array_equal(got3, ref3)
+    A2, B2, X2 = O.ns_iteration(X, round_once=True)
+    assert np.array_equal(A2, A) and np.array_equal(B2, Bm)
+    assert np.array_equal(X2, O.bmm_add(Bm, X, a, round_once=True))
+
+
+def test_staged_2d_is_a_distinct_rounding_within_bf16_of_exact():
+    G = _well_conditioned((96, 160), 5).astype(np.float32)
+    exact = O.ns5_fp64(G)
+    s2, s3 = O.ns5_staged_2d(G), O.ns5_staged(G)
+    assert _rel_fro(s2, exact) < 3e-2 and _rel_fro(s3, exact) < 3e-2
+    assert not np.array_equal(s2, s3)
+    assert np.array_equal(O.bf16_round(s2), s2)
