@@ -41,6 +41,7 @@ PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 4096 FLOP/clk x 2.
 
 # NS stage kernels per kernel family, per NS iteration.
 NS_KERNELS = {
+    "fused": "ns5 stage: ns_st_kernel<0> (X X^T) + ns_ba_kernel (c A A^T + b A, then B X + a X with B kept in LDS) per iteration",
     "stream": "ns5 stage: ns_st_kernel<0> (X X^T), <1> (c A A^T + b A), <2> (B X + a X) per iteration",
     "lds": "ns5 stage: ns5_lds_kernel (all 5 iterations of a 128-row tile resident in LDS)",
     "small": "ns5 stage: ns_gram_kernel x2 + ns_apply_kernel per iteration",
@@ -50,14 +51,17 @@ NS_KERNELS = {
 def ns_family(mp: int, np_: int, family: str = "auto") -> str:
     """The NS kernel family the library runs for an (mp, np) tile buffer
     (himuon_ns5_ex dispatch): with family "block128" the 128-blocks
-    everywhere; with "auto", LDS-resident for mp == 128 and np <= 256,
-    streamed 256-blocks for edges that are multiples of 256, else 128-blocks."""
+    everywhere; with "stream3" the three streamed 256-block products wherever
+    both edges are multiples of 256; with "auto", LDS-resident for mp == 128
+    and np <= 256, the Gram kernel plus the fused GramB/Apply kernel for
+    512 x 512 tiles, streamed 256-blocks for other multiples of 256, else
+    128-blocks."""
     if family == "block128":
         return "small"
     if mp == 128 and np_ in (128, 256):
         return "lds"
     if mp % 256 == 0 and np_ % 256 == 0:
-        return "stream"
+        return "fused" if (family == "auto" and mp == 512 and np_ == 512) else "stream"
     return "small"
 
 
@@ -115,10 +119,15 @@ def algorithmic_flops(opt) -> float:
 
 def time_ns_stage(opt, reps: int) -> float:
     """Average ms of the NS5 stage of one step (all chunks of all groups),
-    HIP events on the stream the kernels are launched on."""
+    HIP events on the stream the kernels are launched on. Each rep first
+    re-gathers the tiles (untimed), so NS always starts from normalised
+    momentum tiles as in a step, not from the previous rep's output."""
     s = torch.cuda.current_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+
+    def gather():
+        for g in opt._groups:
+            g["tiles"].gather()
 
     def run():
         for g in opt._groups:
@@ -127,14 +136,16 @@ def time_ns_stage(opt, reps: int) -> float:
                 g["tiles"].ns(ofs, c, g["steps"], opt._workspace, g["sub_batch"])
                 ofs += c
 
+    gather()
     run()
     torch.cuda.synchronize()
-    e0.record(s)
-    for _ in range(reps):
+    for e0, e1 in evs:
+        gather()
+        e0.record(s)
         run()
-    e1.record(s)
-    e1.synchronize()
-    return e0.elapsed_time(e1) / reps
+        e1.record(s)
+    torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in evs) / reps
 
 
 def time_io_stage(opt, reps: int) -> tuple[float, float]:

@@ -237,8 +237,9 @@ def ns5_workspace_bytes(sub_batch: int, mp: int, np_: int) -> int:
 # runs). ROUND_ONCE: the reference's 2-D third product, bf16(B X + a X).
 NS_FAMILY_AUTO = 0
 NS_FAMILY_BLOCK128 = 1
+NS_FAMILY_STREAM3 = 2
 NS_ROUND_ONCE = 0x10
-NS_FAMILIES = {"auto": NS_FAMILY_AUTO, "block128": NS_FAMILY_BLOCK128}
+NS_FAMILIES = {"auto": NS_FAMILY_AUTO, "block128": NS_FAMILY_BLOCK128, "stream3": NS_FAMILY_STREAM3}
 # Family every ns5() call runs unless it names one: "auto". Tests and
 # benchmarks that compare families set this attribute; the optimizer never does.
 ns_family_override = "auto"

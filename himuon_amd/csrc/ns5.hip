@@ -296,7 +296,8 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
   if (!x || !y || x == y || !inv || n_tiles < 0 || steps < 0 || mp <= 0 || np <= 0 || mp > np ||
       mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN || sub_batch <= 0 ||
       (flags & ~(HIMUON_NS_FAMILY_MASK | HIMUON_NS_ROUND_ONCE)) ||
-      (family != HIMUON_NS_FAMILY_AUTO && family != HIMUON_NS_FAMILY_BLOCK128))
+      (family != HIMUON_NS_FAMILY_AUTO && family != HIMUON_NS_FAMILY_BLOCK128 &&
+       family != HIMUON_NS_FAMILY_STREAM3))
     return HIMUON_EINVAL;
   if (n_tiles == 0) return 0;
   const int64_t sb = sub_batch < n_tiles ? sub_batch : n_tiles;
@@ -320,9 +321,12 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
   // and np <= 256 run the fused LDS-resident kernel (ns5_lds.hip); other tiles
   // run the 128-block kernels below, which family BLOCK128 selects for every
   // geometry.
+  // 512 x 512 tiles run the first product on the stream kernels and the
+  // other two fused (ns5_ba.hip); family STREAM3 keeps three stream kernels.
   const bool small = family == HIMUON_NS_FAMILY_BLOCK128;
   const bool st = ns5_stream_supported(mp, np) && !small;
   const bool lds = ns5_lds_supported(mp, np) && !small;
+  const bool ba = ns5_ba_supported(mp, np) && family == HIMUON_NS_FAMILY_AUTO;
   const int nb = mp / BM;
   const int npairs = nb * (nb + 1) / 2;
   const int apply_blocks = (mp / BM) * (np / BN);
@@ -333,7 +337,7 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
     if (lds) {
       ns5_lds_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, s);
     } else if (st) {
-      ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, wsA, wsB, s);
+      ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, ba, wsA, wsB, s);
     } else {
       const uint16_t* cur = x + o;
       uint16_t* nxt = y + o;

@@ -1,0 +1,401 @@
+// Fused second and third NS products for 512 x 512 NS tiles ("BA" kernel):
+//
+//   B  = bf16(c A A^T + b A)                  (ba_plus_cAA.py:58-85)
+//   X' = bf16(bf16(B X) + a X)                (fused_bmm_add.py:65-88)
+//        bf16(B X + a X) with round_once      (torch.addmm, himuon.py:249-253)
+//
+// one 128-row panel of one tile per work item, so that B never leaves the
+// CU: per tile and iteration HBM carries A and X in and X' out (1.5 MiB)
+// instead of A in, B out, B and X in and X' out (2.5 MiB). The first product
+// (A = bf16(X X^T)) stays the streamed Gram kernel (ns5_stream.hip).
+//
+// Work item (tile t, panel p), rows i0 = 128 p .. i0 + 127, four waves; wave
+// w owns output columns 128 w .. 128 w + 127 in both stages, as 4 x 4
+// v_mfma_f32_32x32x16_bf16 tiles (256 fp32 accumulators per lane, one wave
+// per SIMD). Items are spread persistently, a contiguous range per XCD.
+//
+//  Stage 1: B_P[i][j] = bf16(c sum_k A[i0+i][k] A[j][k] + b A[i0+i][j]).
+//    Row-side operand A_P (128 x 512 bf16 = 128 KiB) resident in LDS region
+//    R, loaded with direct-to-LDS DMA right after the previous item's last
+//    read of R. Column-side operand: A is exactly symmetric, so A[j][k] =
+//    A[k][j] and the wave streams rows k of A restricted to its 128 columns.
+//  Stage 2: X'_P[i][j] = bf16(bf16(sum_k B_P[i][k] X[k][j]) + a X[i0+i][j]).
+//    Row-side operand B_P, written over A_P in R by the stage-1 epilogue;
+//    column-side operand: rows k of X restricted to the wave's columns.
+//
+//  Both K loops run the same schedule: the streamed rows go from global
+//  memory into a four-unit register ring (a unit = 32 rows = two k-steps of
+//  16, 8 x 16-byte loads per lane), three units ahead of the MFMAs; each
+//  k-step's 16 rows are written to one of two wave-private 4 KiB staging
+//  buffers and read back as column fragments with ds_read_b64_tr_b16
+//  (contraction along the rows). No workgroup barrier inside a loop: the
+//  staging buffers are private and a wave's LDS operations execute in order.
+//  After stage 2 the ring carries the X_P rows i0 .. i0 + 127 (the a X term).
+//
+//  Stage-1 epilogue: B_P = bf16(c acc + b A_P) for the wave's own columns,
+//  read from and written to the same R addresses, between two barriers.
+//  Stage-2 epilogue, per 32-row block: X_P into the accumulator layout
+//  through the wave's 8 KiB staging area, the result back through it into
+//  256-byte row stores, and the next item's first ring units loaded.
+//
+// Per item the waves meet at four barriers: A_P landed, A_P reads done, B_P
+// written, B_P reads done (R free for the next item's DMA). Each output
+// element sums its k terms in one fp32 accumulator in ascending k with the
+// same MFMA as the three-kernel path, so results are bit-identical to it.
+//
+// LDS: R (128 KiB, fragment-major, below), then a 8 KiB area per wave (two
+// 4 KiB staging buffers: 16 rows x 256 B, chunk c of row r at c ^ 4 (r % 4),
+// conflict-free for row writes and transposing reads; epilogue: 32 rows x
+// 256 B, chunk c of row r at c ^ (r % 16)).
+#include "ns5_kernels.h"
+
+namespace {
+
+constexpr int T = 512;           // tile edge (mp = np)
+constexpr int P = 128;           // panel rows
+constexpr int NW = 4;            // waves
+constexpr int NTH = 64 * NW;
+constexpr int R_BYTES = P * T * 2;          // 128 KiB
+constexpr int WAREA = 8192;                 // per-wave staging
+constexpr int LDS_BYTES = R_BYTES + NW * WAREA;
+constexpr int NKS = T / 16;                 // k-steps per stage
+constexpr int NUNIT = T / 32;               // ring units per stage (2 k-steps each)
+constexpr int NSLOT = 4;                    // ring slots
+constexpr int AHEAD = NSLOT - 1;            // units in flight ahead of the MFMAs
+static_assert(LDS_BYTES == 160 * 1024, "LDS budget");
+
+struct BaArgs {
+  const uint16_t* A;   // (ntiles, T, T) bf16, symmetric
+  const uint16_t* X;   // (ntiles, T, T) bf16
+  uint16_t* Y;         // (ntiles, T, T) bf16 output X'
+  int64_t ntiles;
+  float a, b, c;
+  int round_once;
+};
+
+typedef __attribute__((address_space(3))) u32x4_t lds_u32x4;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+HM_DEV u32x2_t read_tr(const lds_u8* p) {
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)p);
+  return __builtin_bit_cast(u32x2_t, r);
+}
+
+// 16 bytes at a wave-uniform base plus a 32-bit byte offset (the
+// scalar-base + vector-offset form of the load: no 64-bit address per lane).
+HM_DEV u32x4_t gload16(const uint16_t* base, uint32_t off) {
+  return *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(base) + off);
+}
+HM_DEV void gstore16(uint16_t* base, uint32_t off, u32x4_t v) {
+  *reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(base) + off) = v;
+}
+
+// One ring unit: 8 x 16 bytes per lane.
+struct Unit {
+  u32x4_t v[8];
+};
+
+// Region R holds a 128 x 512 panel (A_P, then B_P) fragment-major: fragment
+// (ti, ks) (rows 32 ti .. + 31, k = 16 ks .. + 15) is 1 KiB at (4 ks + ti) KiB,
+// lane l's 16 bytes (row 32 ti + l % 32, k = 16 ks + 8 (l / 32) .. + 7) at
+// 16 l: one lane base plus an immediate per fragment, conflict-free.
+HM_DEV int frag_off(int ti, int ks) { return (4 * ks + ti) * 1024; }
+
+template <bool ROUND_ONCE>
+__global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[LDS_BYTES];
+  lds_u8* const lds = (lds_u8*)lds_raw;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
+  const int l32 = lane & 31, hi = lane >> 5;
+  const uint32_t r_base = (uint32_t)(uintptr_t)lds;
+  // lane base of the R fragments (fragment offsets added per k-step)
+  const lds_u8* const Rl0 = lds + 16 * lane;
+  lds_u8* const W = lds + R_BYTES + wave * WAREA;
+  // Row staging: two 4 KiB buffers (k-steps ks % 2), 16 rows x 256 bytes,
+  // 16-byte chunk c of row r at c ^ 4 (r % 4) (conflict-free for the row
+  // writes and the transposing reads). Row writes: lane base xw + 1 KiB n;
+  // transposing reads of column fragment tj: lane base xr[tj] (+ 1 KiB for
+  // k-rows 4..7 of the lane's eight).
+  lds_u8* const xw = W + 256 * (lane >> 4) + (((lane & 15) ^ (4 * (lane >> 4))) << 4);
+  const int tr_m = (lane & 15) >> 2;
+  const lds_u8* const xr0 = W + 256 * (8 * hi + tr_m) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3);
+  // epilogue staging (32 rows x 256 B, chunk c of row r at c ^ (r & 15))
+  auto ep_off = [](int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); };
+
+  // (32-bit item indices: the launcher takes at most 2^29 tiles per call)
+  const int total = (int)g.ntiles * (T / P);
+  const int wper = (int)(gridDim.x >> 3);
+  const int per_xcd = (total + 7) >> 3;
+  const int ibeg = (int)(blockIdx.x & 7) * per_xcd;
+  const int iend = (ibeg + per_xcd < total) ? ibeg + per_xcd : total;
+  int item = ibeg + (int)(blockIdx.x >> 3);
+  if (item >= iend) return;
+
+  // ---- operand sources ----------------------------------------------------------
+  // Both stages stream k-rows of a 512 x 512 bf16 matrix restricted to the
+  // wave's 128 columns: stage 1 rows of A (A is exactly symmetric, so its
+  // row k holds column k: A[k][j] = A[j][k], the B-operand of c A_P A^T),
+  // stage 2 rows of X. A ring unit is 32 rows: lane l holds row row0 + 4 n +
+  // l / 16, columns 128 w + 8 (l % 16) .. + 7, in v[n] (n = 0..7). The uniform
+  // part of each address goes into the scalar base, the lane part is one
+  // 32-bit offset (a tile is 512 KiB).
+  const uint32_t x_lane = 2u * ((lane >> 4) * T + 128 * wave + 8 * (lane & 15));
+  auto load_row = [&](const uint16_t* M, int row0, Unit& d, int n) { d.v[n] = gload16(M + (row0 + 4 * n) * T, x_lane); };
+  auto load_rows = [&](const uint16_t* M, int row0, Unit& d) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) load_row(M, row0, d, n);
+  };
+  // A_P into R, fragment-major: one 1 KiB fragment per instruction. Call q
+  // (0..3) loads the fragments of k-steps 8 q .. 8 q + 7: wave w takes k-steps
+  // 8 q + 2 w, 8 q + 2 w + 1, every ti (ln, wv: the lane and wave index,
+  // opaque per call so the addresses are formed where they are used).
+  auto dma_ap = [&](const uint16_t* At, int i0, int q, int ln, int wv) {
+    const uint16_t* src = At + (i0 + (ln & 31)) * T + 8 * (ln >> 5) + 16 * (8 * q + 2 * wv);
+    const uint32_t dst = r_base + frag_off(0, 8 * q + 2 * wv);
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) dma16(src + 32 * ti * T + 16 * k, dst + frag_off(ti, k));
+  };
+
+  Unit ring[NSLOT];
+  {
+    const uint16_t* At = g.A + (item >> 2) * (int64_t)T * T;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma_ap(At, P * (int)(item & 3), q, lane, wave);
+#pragma unroll
+    for (int u = 0; u < AHEAD; ++u) load_rows(At, 32 * u, ring[u]);
+  }
+  const float ca = g.a, cb = g.b, cc = g.c;
+
+  for (;;) {
+    // The lane index, opaque per item: lane-dependent addresses are formed
+    // inside the item loop, not hoisted out of it for the whole kernel (they
+    // would not fit in the registers left beside the ring and accumulators).
+    // (read by volatile assembly: a pure builtin would be hoisted and held.)
+    int lane_o, wave_o = wave;
+    uint32_t xl_o = x_lane;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_o));
+    asm volatile("" : "+s"(wave_o), "+v"(xl_o));
+    const int64_t tile = item >> 2;
+    const int i0 = P * (int)(item & 3);
+    const uint16_t* At = g.A + tile * (int64_t)T * T;
+    const uint16_t* Xt = g.X + tile * (int64_t)T * T;
+    uint16_t* Yt = g.Y + tile * (int64_t)T * T;
+    const int next = item + wper;
+    const bool more = next < iend;
+
+    // A_P landed: the 24 ring loads of units 0..2 were issued after its DMA.
+    wait_vm<3 * 8>();
+    lds_barrier();
+
+    f32x16_t acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+
+    // ---- one K loop: acc += P_frag x (rows of M) over k = 0..511 ----------------------
+    // k-step ks: its 16 rows (ring unit ks / 2, registers 4 (ks % 2) ..) go to
+    // staging buffer ks % 2 and come back as column fragments through
+    // transposing reads; the row fragments of the panel (A_P or B_P) come from
+    // R. While k-step ks's four MFMA rows run: after rows 0..2, k-step ks + 1's
+    // reads (the R fragments first, every MFMA row needs them; then the
+    // transposing reads); after row 3, k-step ks + 2's rows into buffer ks % 2,
+    // behind those reads (a wave's LDS operations execute in order); after
+    // each row, one load of the unit three ahead.
+    u32x4_t fa[2][4], fb[2][4];
+    auto read_frags = [&](int ks, int b, int part) {
+      const int buf = 4096 * (ks & 1);
+      if (part == 0) {
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) fb[b][ti] = *reinterpret_cast<const lds_u32x4*>(Rl0 + frag_off(ti, ks));
+      } else {
+#pragma unroll
+        for (int t2 = 2 * (part - 1); t2 < 2 * (part - 1) + 2; ++t2) {
+          const lds_u8* p = xr0 + buf + ((t2 ^ tr_m) << 6);
+          const u32x2_t lo = read_tr(p);
+          const u32x2_t up = read_tr(p + 1024);
+          fa[b][t2] = u32x4_t{lo[0], lo[1], up[0], up[1]};
+        }
+      }
+    };
+    auto write_rows = [&](int ks, const Unit& su) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+        *reinterpret_cast<lds_u32x4*>(xw + 4096 * (ks & 1) + 1024 * n) = su.v[4 * (ks & 1) + n];
+    };
+    // stream unit v of this item: stage-1 A rows (v < 16), stage-2 X rows
+    // (16 <= v < 32), then the X_P rows i0 .. i0 + 127 (v >= 32)
+    auto unit_src = [&](int v, const uint16_t*& M, int& row0) {
+      M = v < NUNIT ? At : Xt;
+      row0 = v < NUNIT ? 32 * v : v < 2 * NUNIT ? 32 * (v - NUNIT) : i0 + 32 * (v - 2 * NUNIT);
+    };
+    auto kloop = [&](int base) {  // base: stream index of the stage's unit 0 (0 or 16)
+      write_rows(0, ring[base % NSLOT]);
+      write_rows(1, ring[base % NSLOT]);
+#pragma unroll
+      for (int p = 0; p < 3; ++p) read_frags(0, 0, p);
+#pragma unroll
+      for (int u = 0; u < NUNIT; ++u) {
+        const uint16_t* M;
+        int row0;
+        unit_src(base + u + AHEAD, M, row0);
+        Unit& dst = ring[(base + u + AHEAD) % NSLOT];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const int ks = 2 * u + s;
+          const int b = (s + 1) & 1;
+#pragma unroll
+          for (int tj = 0; tj < 4; ++tj) {
+#pragma unroll
+            for (int ti = 0; ti < 4; ++ti) acc[tj][ti] = mfma(fa[s][tj], fb[s][ti], acc[tj][ti]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (tj < 3) {
+              if (ks + 1 < NKS) read_frags(ks + 1, b, tj);
+            } else if (ks + 2 < NKS) {
+              write_rows(ks + 2, ring[(base + u + 1) % NSLOT]);  // unit u + 1, half s
+            }
+            load_row(M, row0, dst, 4 * s + tj);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+    };
+
+    // ---- stage 1: c A_P A^T -----------------------------------------------------------
+    kloop(0);
+
+    // ---- stage-1 epilogue: B_P = bf16(c acc + b A_P) over A_P, own columns ----------
+    // element (i = 32 ti + l32, j = 128 w + 32 tj + 8 q + 4 hi + e) is k = j of
+    // fragment (ti, 8 w + 2 tj + q / 2), lane l32 + 32 (q % 2), bytes 8 hi ..:
+    // lane base plus an immediate.
+    lds_barrier();  // every wave is done reading A_P fragments
+    {
+      lds_u8* const ep1 = lds + 32768 * wave + 16 * (lane_o & 31) + 8 * (lane_o >> 5);
+      auto ep1_off = [](int ti, int tj, int q) { return 8192 * tj + 4096 * (q >> 1) + 512 * (q & 1) + 1024 * ti; };
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        // all 16 A_P pieces of this row block first, one wait, then B_P over them
+        u32x2_t av[4][4];
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            av[tj][q] = *reinterpret_cast<const lds_cu32x2*>(ep1 + ep1_off(ti, tj, q));
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              y[e] = fmaf(cb, bf16_to_f32(half16(av[tj][q][e >> 1], e & 1)), cc * acc[tj][ti][4 * q + e]);
+            *reinterpret_cast<lds_u32x2*>(ep1 + ep1_off(ti, tj, q)) =
+                u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
+          }
+      }
+    }
+    lds_barrier();  // B_P complete
+
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+
+    // ---- stage 2: B_P X ---------------------------------------------------------------
+    kloop(NUNIT);
+    // X_P rows i0 + 96 .. i0 + 127 (the fourth X_P unit) into the slot unit 15 freed
+    load_rows(Xt, i0 + 96, ring[(2 * NUNIT + AHEAD) % NSLOT]);
+    // All X_P units in before the next A_P's DMA is issued: a wait for an
+    // X_P unit after it would also wait for the DMA (vmcnt retires in order).
+    wait_vm<0>();
+    lds_barrier();  // every wave is done reading B_P: R is free
+    const int nitem = next;
+    const uint16_t* nAt = g.A + ((more ? nitem : item) >> 2) * (int64_t)T * T;
+    if (more) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dma_ap(nAt, P * (int)(nitem & 3), q, lane_o, wave_o);
+    }
+
+    // ---- stage-2 epilogue -------------------------------------------------------------
+    // X_P unit q (rows 32 q ..) sits in ring[(2 NUNIT + q) % NSLOT] = ring[q].
+    const int el32 = lane_o & 31, ehi = lane_o >> 5, erow = lane_o >> 4, ech = lane_o & 15;
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      const Unit& xp = ring[(2 * NUNIT + ti) % NSLOT];
+#pragma unroll
+      for (int n = 0; n < 8; ++n)
+        *reinterpret_cast<lds_u32x4*>(W + ep_off(4 * n + erow, ech)) = xp.v[n];
+      // X_P in the accumulator layout: all 16 pieces, one wait
+      u32x2_t xv[4][4];
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          xv[tj][q] = *reinterpret_cast<const lds_cu32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi);
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float y[4], bx[4];
+#pragma unroll
+          for (int e = 0; e < 4; e += 2) {
+            const float v0 = acc[tj][ti][4 * q + e], v1 = acc[tj][ti][4 * q + e + 1];
+            if constexpr (ROUND_ONCE) {
+              bx[e] = v0;
+              bx[e + 1] = v1;
+            } else {  // bf16(B X), two at a time
+              const uint32_t r = pk_bf16(v0, v1);
+              bx[e] = __uint_as_float(r << 16);
+              bx[e + 1] = __uint_as_float(r & 0xffff0000u);
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = fmaf(ca, bf16_to_f32(half16(xv[tj][q][e >> 1], e & 1)), bx[e]);
+          *reinterpret_cast<lds_u32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi) =
+              u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
+        }
+      // the 32 result rows: all 8 row reads, one wait, 8 row stores
+      u32x4_t rows[8];
+#pragma unroll
+      for (int n = 0; n < 8; ++n) rows[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(4 * n + erow, ech));
+#pragma unroll
+      for (int n = 0; n < 8; ++n) gstore16(Yt + (i0 + 32 * ti + 4 * n) * T, xl_o, rows[n]);
+      // the next item's stage-1 units 0..2 into the slots X_P units 0..2 freed
+      if (more && ti < AHEAD) load_rows(nAt, 32 * ti, ring[ti]);
+    }
+    if (!more) break;
+    item = nitem;
+  }
+}
+
+int num_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  return n;
+}
+
+}  // namespace
+
+bool ns5_ba_supported(int mp, int np) { return mp == T && np == T; }
+
+void ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, int64_t cnt, float a, float b, float c,
+                bool round_once, hipStream_t s) {
+  const int64_t items = cnt * (T / P);
+  const int64_t per_xcd = (items + 7) / 8;
+  const int64_t wgs_per_xcd = std::max<int64_t>(1, std::min<int64_t>(num_cus() / 8, per_xcd));
+  const BaArgs args{A, X, Y, cnt, a, b, c, round_once ? 1 : 0};
+  if (round_once)
+    hipLaunchKernelGGL(ns_ba_kernel<true>, dim3((unsigned)(8 * wgs_per_xcd)), dim3(NTH), 0, s, args);
+  else
+    hipLaunchKernelGGL(ns_ba_kernel<false>, dim3((unsigned)(8 * wgs_per_xcd)), dim3(NTH), 0, s, args);
+}

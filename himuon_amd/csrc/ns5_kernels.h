@@ -71,6 +71,32 @@ HM_DEV u32x2_t ds_read_tr16(uint32_t addr) {
   return r;
 }
 
+// Workgroup barrier for LDS reuse: this wave's LDS operations are complete;
+// global memory operations (including direct-to-LDS loads) may still be in
+// flight and are waited for explicitly with vmcnt. (__syncthreads() lowers
+// to a fence that waits for every outstanding load and store, which would
+// drain the operand stream at each barrier.)
+HM_DEV void lds_barrier() {
+  wait_lgkm<0>();
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// Direct-to-LDS 16-byte load: lane l's 16 bytes from gptr land at LDS byte
+// lds_wave + 16 l (lds_wave is wave-uniform, passed in M0). Issued as inline
+// assembly: the compiler models the builtin as a flat access to both global
+// memory and LDS and, while one is pending, forces lgkmcnt(0)/vmcnt(0) waits
+// before unrelated LDS reads. Completion is tracked by vmcnt (in issue order
+// with the other vector loads) and waited for explicitly.
+HM_DEV void dma16(const void* gptr, uint32_t lds_wave) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(gptr), "s"(__builtin_amdgcn_readfirstlane(lds_wave))
+      : "memory", "m0");
+}
+
 // DPP quad permutations.
 HM_DEV uint32_t quad_swap2(uint32_t v) {  // lane ^ 2
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
@@ -105,10 +131,18 @@ HM_DEV u32x2_t quad_transpose(u32x2_t w, int k) {
 // multiples of 256. Scales x in place (X0), then runs `steps` iterations on
 // `cnt` tiles, ping-ponging X between x and y. round_once: the third product
 // rounds bf16(B X + a X) once (the 2-D form) instead of bf16(bf16(B X) + a X).
+// fused_ba: the second and third products run as one kernel (ns5_ba.hip;
+// mp == np == 512), wsB unused.
 bool ns5_stream_supported(int mp, int np);
 void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
-                    float a, float b, float c, bool round_once, uint16_t* wsA, uint16_t* wsB,
+                    float a, float b, float c, bool round_once, bool fused_ba, uint16_t* wsA, uint16_t* wsB,
                     hipStream_t s);
+
+// Fused B = bf16(c A A^T + b A), Y = bf16(bf16(B X) + a X) (ns5_ba.hip) on
+// `cnt` 512 x 512 tiles: A from the first product, X -> Y (Y != X).
+bool ns5_ba_supported(int mp, int np);
+void ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, int64_t cnt, float a, float b, float c,
+                bool round_once, hipStream_t s);
 
 // One NS product over `ntiles` batch entries on the 256-block stream kernels
 // (M, N, K multiples of 256; row pitches in elements, batch strides):

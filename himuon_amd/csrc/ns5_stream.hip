@@ -61,32 +61,6 @@ struct StArgs {
   int round_once;                              // Apply: bf16(B X + a X), one rounding
 };
 
-// Workgroup barrier for LDS reuse: this wave's LDS operations are complete;
-// global memory operations (including direct-to-LDS loads) may still be in
-// flight and are waited for explicitly with vmcnt. (__syncthreads() lowers
-// to a fence that waits for every outstanding load and store, which would
-// drain the operand stream at each barrier.)
-HM_DEV void lds_barrier() {
-  wait_lgkm<0>();
-  asm volatile("s_barrier" ::: "memory");
-}
-
-// Direct-to-LDS 16-byte load: lane l's 16 bytes from gptr land at LDS byte
-// lds_wave + 16 l (lds_wave is wave-uniform, passed in M0). Issued as inline
-// assembly: the compiler models the builtin as a flat access to both global
-// memory and LDS and, while one is pending, forces lgkmcnt(0)/vmcnt(0) waits
-// before unrelated LDS reads. Completion is tracked by vmcnt (in issue order
-// with the other vector loads) and waited for explicitly.
-HM_DEV void dma16(const void* gptr, uint32_t lds_wave) {
-  asm volatile(
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
-      :
-      : "v"(gptr), "s"(__builtin_amdgcn_readfirstlane(lds_wave))
-      : "memory", "m0");
-}
-
 // Chunk swizzles (16-byte chunk index XOR a function of the row):
 //  P/Q row panels, 64-byte rows: spreads 8 (or 16) consecutive rows of one
 //  chunk over distinct bank groups for 32- and 64-bank layouts;
@@ -588,7 +562,7 @@ void ns_stream_product(int mode, const uint16_t* P, int64_t p_bs, int ldp, const
 // between x and y (x is scaled in place first); A and B live in the
 // workspace.
 void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
-                    float a, float b, float c, bool round_once, uint16_t* wsA, uint16_t* wsB,
+                    float a, float b, float c, bool round_once, bool fused_ba, uint16_t* wsA, uint16_t* wsB,
                     hipStream_t s) {
   const int64_t sq = (int64_t)mp * mp, rect = (int64_t)mp * np;
   const int nb = mp / BT;
@@ -602,6 +576,11 @@ void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int
   for (int it = 0; it < steps; ++it) {
     const StArgs ga{cur, rect, np, cur, rect, np, nullptr, 0, 0, wsA, sq, mp, mp, mp, np, cnt, 1.0f, 0.0f, 0};
     launch<kGramA>(ga, gram_items, s);
+    if (fused_ba) {  // B stays on chip: ns5_ba.hip
+      ns5_ba_run(wsA, cur, nxt, cnt, a, b, c, round_once, s);
+      std::swap(cur, nxt);
+      continue;
+    }
     const StArgs gb{wsA, sq, mp, wsA, sq, mp, wsA, sq, mp, wsB, sq, mp, mp, mp, mp, cnt, c, b, 0};
     launch<kGramB>(gb, gram_items, s);
     const StArgs ap{wsB, sq, mp, cur, rect, np, cur, rect, np, nxt, rect, np, mp, np, mp, cnt, 1.0f, a, round_once ? 1 : 0};

@@ -157,12 +157,15 @@ int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles,
  *  - kernel family (bits HIMUON_NS_FAMILY_MASK; no reference counterpart,
  *    for comparison tests and benchmarks): HIMUON_NS_FAMILY_AUTO picks per
  *    geometry as himuon_ns5 does; HIMUON_NS_FAMILY_BLOCK128 runs the
- *    128x128-block kernels for every geometry. Results are identical.
+ *    128x128-block kernels for every geometry; HIMUON_NS_FAMILY_STREAM3 runs
+ *    the three products as three streamed 256-block kernels where AUTO fuses
+ *    the second and third (512 x 512 tiles). Results are identical.
  * Any other flag bit is an argument error.
  */
 #define HIMUON_NS_FAMILY_MASK 0x0F
 #define HIMUON_NS_FAMILY_AUTO 0
 #define HIMUON_NS_FAMILY_BLOCK128 1
+#define HIMUON_NS_FAMILY_STREAM3 2
 #define HIMUON_NS_ROUND_ONCE 0x10
 int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles,
                   int mp, int np, int steps, float a, float b, float c,

@@ -18,8 +18,10 @@ def test_ns_family_follows_the_library_dispatch():
     # LDS-resident kernel: mp == 128 and np <= 256
     assert bench.ns_family(128, 128) == "lds"
     assert bench.ns_family(128, 256) == "lds"
+    # 512 x 512: Gram kernel + fused GramB/Apply; the three products with "stream3"
+    assert bench.ns_family(512, 512) == "fused"
+    assert bench.ns_family(512, 512, "stream3") == "stream"
     # streamed 256-blocks: both padded edges multiples of 256
-    assert bench.ns_family(512, 512) == "stream"
     assert bench.ns_family(256, 1024) == "stream"
     assert bench.ns_family(1024, 3072) == "stream"
     # everything else: 128-block kernels
@@ -27,7 +29,7 @@ def test_ns_family_follows_the_library_dispatch():
     assert bench.ns_family(640, 768) == "small"
     assert bench.ns_family(384, 384) == "small"
     assert bench.ns_family(512, 512, "block128") == "small"
-    assert set(bench.NS_KERNELS) == {"stream", "lds", "small"}
+    assert set(bench.NS_KERNELS) == {"fused", "stream", "lds", "small"}
 
 
 def test_ns_flops_is_the_normative_count():

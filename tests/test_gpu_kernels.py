@@ -69,11 +69,13 @@ GATHER_CASES = [
 ]
 
 
-@pytest.fixture(params=["auto", "block128"])
+@pytest.fixture(params=["auto", "stream3", "block128"])
 def ns_family(request, monkeypatch):
     """Run a test under each NS kernel family selection: "auto" (the
-    product's per-geometry choice: LDS-resident, persistent streamed 256-blocks
-    or 128-blocks) and "block128" (the 128-block kernels for every geometry)."""
+    product's per-geometry choice: LDS-resident, the fused GramB/Apply kernel
+    for 512 x 512 tiles, persistent streamed 256-blocks or 128-blocks),
+    "stream3" (the three streamed products where AUTO fuses two) and
+    "block128" (the 128-block kernels for every geometry)."""
     monkeypatch.setattr(nat, "ns_family_override", request.param)
     return request.param
 
