@@ -71,6 +71,7 @@ struct BaArgs {
   int64_t ntiles;
   float a, b, c;
   int round_once;
+  const float* xinv;   // SC: X is the raw tile, X0 = bf16(X xinv[tile]) used in its place
 };
 
 typedef __attribute__((address_space(3))) u32x4_t lds_u32x4;
@@ -102,7 +103,9 @@ struct Unit {
 // 16 l: one lane base plus an immediate per fragment, conflict-free.
 HM_DEV int frag_off(int ti, int ks) { return (4 * ks + ti) * 1024; }
 
-template <bool ROUND_ONCE>
+// SC (the first iteration): every X value (stage-2 rows, the a X term) is
+// replaced by bf16(x xinv[tile]) before it is used.
+template <bool ROUND_ONCE, bool SC>
 __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[LDS_BYTES];
   lds_u8* const lds = (lds_u8*)lds_raw;
@@ -186,6 +189,8 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     uint16_t* Yt = g.Y + tile * (int64_t)T * T;
     const int next = item + wper;
     const bool more = next < iend;
+    float xs = 1.f;
+    if constexpr (SC) xs = g.xinv[tile];
 
     // A_P landed: the 24 ring loads of units 0..2 were issued after its DMA.
     wait_vm<3 * 8>();
@@ -224,10 +229,13 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
         }
       }
     };
-    auto write_rows = [&](int ks, const Unit& su) {
+    auto write_rows = [&](int ks, const Unit& su, bool xrows) {
 #pragma unroll
-      for (int n = 0; n < 4; ++n)
-        *reinterpret_cast<lds_u32x4*>(xw + 4096 * (ks & 1) + 1024 * n) = su.v[4 * (ks & 1) + n];
+      for (int n = 0; n < 4; ++n) {
+        u32x4_t v = su.v[4 * (ks & 1) + n];
+        if (SC && xrows) v = scale8_rne(v, xs);
+        *reinterpret_cast<lds_u32x4*>(xw + 4096 * (ks & 1) + 1024 * n) = v;
+      }
     };
     // stream unit v of this item: stage-1 A rows (v < 16), stage-2 X rows
     // (16 <= v < 32), then the X_P rows i0 .. i0 + 127 (v >= 32)
@@ -236,8 +244,9 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
       row0 = v < NUNIT ? 32 * v : v < 2 * NUNIT ? 32 * (v - NUNIT) : i0 + 32 * (v - 2 * NUNIT);
     };
     auto kloop = [&](int base) {  // base: stream index of the stage's unit 0 (0 or 16)
-      write_rows(0, ring[base % NSLOT]);
-      write_rows(1, ring[base % NSLOT]);
+      const bool xrows = base == NUNIT;  // stage 2 streams X
+      write_rows(0, ring[base % NSLOT], xrows);
+      write_rows(1, ring[base % NSLOT], xrows);
 #pragma unroll
       for (int p = 0; p < 3; ++p) read_frags(0, 0, p);
 #pragma unroll
@@ -258,7 +267,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
             if (tj < 3) {
               if (ks + 1 < NKS) read_frags(ks + 1, b, tj);
             } else if (ks + 2 < NKS) {
-              write_rows(ks + 2, ring[(base + u + 1) % NSLOT]);  // unit u + 1, half s
+              write_rows(ks + 2, ring[(base + u + 1) % NSLOT], xrows);  // unit u + 1, half s
             }
             load_row(M, row0, dst, 4 * s + tj);
             __builtin_amdgcn_sched_barrier(0);
@@ -332,7 +341,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
       const Unit& xp = ring[(2 * NUNIT + ti) % NSLOT];
 #pragma unroll
       for (int n = 0; n < 8; ++n)
-        *reinterpret_cast<lds_u32x4*>(W + ep_off(4 * n + erow, ech)) = xp.v[n];
+        *reinterpret_cast<lds_u32x4*>(W + ep_off(4 * n + erow, ech)) = SC ? scale8_rne(xp.v[n], xs) : xp.v[n];
       // X_P in the accumulator layout: all 16 pieces, one wait
       u32x2_t xv[4][4];
 #pragma unroll
@@ -388,14 +397,19 @@ int num_cus() {
 
 bool ns5_ba_supported(int mp, int np) { return mp == T && np == T; }
 
-void ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, int64_t cnt, float a, float b, float c,
-                bool round_once, hipStream_t s) {
+void ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, const float* xinv, int64_t cnt, float a,
+                float b, float c, bool round_once, hipStream_t s) {
   const int64_t items = cnt * (T / P);
   const int64_t per_xcd = (items + 7) / 8;
   const int64_t wgs_per_xcd = std::max<int64_t>(1, std::min<int64_t>(num_cus() / 8, per_xcd));
-  const BaArgs args{A, X, Y, cnt, a, b, c, round_once ? 1 : 0};
-  if (round_once)
-    hipLaunchKernelGGL(ns_ba_kernel<true>, dim3((unsigned)(8 * wgs_per_xcd)), dim3(NTH), 0, s, args);
+  const BaArgs args{A, X, Y, cnt, a, b, c, round_once ? 1 : 0, xinv};
+  const dim3 grid((unsigned)(8 * wgs_per_xcd));
+  if (round_once && xinv)
+    hipLaunchKernelGGL((ns_ba_kernel<true, true>), grid, dim3(NTH), 0, s, args);
+  else if (round_once)
+    hipLaunchKernelGGL((ns_ba_kernel<true, false>), grid, dim3(NTH), 0, s, args);
+  else if (xinv)
+    hipLaunchKernelGGL((ns_ba_kernel<false, true>), grid, dim3(NTH), 0, s, args);
   else
-    hipLaunchKernelGGL(ns_ba_kernel<false>, dim3((unsigned)(8 * wgs_per_xcd)), dim3(NTH), 0, s, args);
+    hipLaunchKernelGGL((ns_ba_kernel<false, false>), grid, dim3(NTH), 0, s, args);
 }

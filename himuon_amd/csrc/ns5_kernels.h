@@ -49,6 +49,15 @@ HM_DEV uint32_t pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// x -> bf16(x * s) for 8 packed bf16 values with the hardware RNE
+// conversion (equal to scale8 for every finite product).
+HM_DEV u32x4_t scale8_rne(u32x4_t v, float s) {
+  u32x4_t o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = pk_bf16(__uint_as_float(v[k] << 16) * s, __uint_as_float(v[k] & 0xffff0000u) * s);
+  return o;
+}
+
 // s_waitcnt with vmcnt = N (expcnt and lgkmcnt at their maxima) / lgkmcnt = N.
 template <int N>
 HM_DEV void wait_vm() {
@@ -128,8 +137,9 @@ HM_DEV u32x2_t quad_transpose(u32x2_t w, int k) {
 
 
 // Persistent streamed-operand 256-block path (ns5_stream.hip): mp, np
-// multiples of 256. Scales x in place (X0), then runs `steps` iterations on
-// `cnt` tiles, ping-ponging X between x and y. round_once: the third product
+// multiples of 256. Runs `steps` iterations on `cnt` tiles from the raw x
+// (the first iteration scales X0 = bf16(x inv) on load), ping-ponging X
+// between x and y. round_once: the third product
 // rounds bf16(B X + a X) once (the 2-D form) instead of bf16(bf16(B X) + a X).
 // fused_ba: the second and third products run as one kernel (ns5_ba.hip;
 // mp == np == 512), wsB unused.
@@ -139,10 +149,12 @@ void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int
                     hipStream_t s);
 
 // Fused B = bf16(c A A^T + b A), Y = bf16(bf16(B X) + a X) (ns5_ba.hip) on
-// `cnt` 512 x 512 tiles: A from the first product, X -> Y (Y != X).
+// `cnt` 512 x 512 tiles: A from the first product, X -> Y (Y != X). xinv
+// non-null: X is the raw tile and X0 = bf16(X xinv[tile]) is used in its
+// place (the first iteration).
 bool ns5_ba_supported(int mp, int np);
-void ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, int64_t cnt, float a, float b, float c,
-                bool round_once, hipStream_t s);
+void ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, const float* xinv, int64_t cnt, float a,
+                float b, float c, bool round_once, hipStream_t s);
 
 // One NS product over `ntiles` batch entries on the 256-block stream kernels
 // (M, N, K multiples of 256; row pitches in elements, batch strides):

@@ -39,7 +39,6 @@
 namespace {
 
 
-constexpr int NT = 256;
 constexpr int BT = 256;               // output block edge
 constexpr int BK = 32;                // K per stream unit
 constexpr int SLOT = 32768;           // bytes per ring slot
@@ -59,6 +58,7 @@ struct StArgs {
   int64_t ntiles;
   float alpha, beta;                           // GramB: c, b; Apply: beta = a
   int round_once;                              // Apply: bf16(B X + a X), one rounding
+  const float* inv;                            // SC kernels: X0 = bf16(X inv[tile]) on load
 };
 
 // Chunk swizzles (16-byte chunk index XOR a function of the row):
@@ -172,7 +172,12 @@ HM_DEV void issue_k(const ItemSrc& s, uint32_t wdst, int v, int slot, bool diag)
 // accumulators per lane, one wave per SIMD). NW = 8: waves in 2 x 4, each
 // 128x64 (4x2 tiles, 128 accumulators, two waves per SIMD, so that one
 // wave's MFMAs can run while the other waits or issues loads).
-template <int MODE, bool DIAG, int NKC, int NW>
+//
+// SC (GramA and Apply of the first iteration): the X operand is the raw
+// tile; every X value is replaced by bf16(x inv[tile]) as it enters the
+// computation (fragments after their LDS reads, the Apply epilogue's a X
+// term), which is X0 exactly as a separate scaling pass would write it.
+template <int MODE, bool DIAG, int NKC, int NW, bool SC>
 __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemPos it, int pre_st,
                                        const bool more, const ItemPos nx) {
   constexpr bool kTr = MODE == kApply;
@@ -194,6 +199,9 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   const int l32 = lane & 31, hi = lane >> 5;
   const int nk = NKC > 0 ? NKC : g.K / BK;  // K units (compile-time for the common K)
   const int U = nk + NR;
+  static_assert(!SC || MODE != kGramB, "GramB has no X operand");
+  float xs = 1.f;
+  if constexpr (SC) xs = g.inv[tile];
 
   // ---- loaders ------------------------------------------------------------
   const ItemSrc src = item_src<MODE, NW>(g, it, lane, wave);
@@ -256,6 +264,27 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     }
   };
 
+  // X0 scaling of landed fragments (SC): GramA both operands, Apply the X one.
+  // Called right after the lgkmcnt wait for these fragments, before further
+  // LDS reads are issued. Apply's fragments come from inline-assembly reads
+  // that the compiler does not track, so each passes through a wait that
+  // names it as an operand: the scaling cannot be scheduled before the data
+  // has landed.
+  auto scale_frags = [&](u32x4_t(&fa)[TJ], u32x4_t(&fb)[4]) {
+    if constexpr (SC) {
+      if constexpr (kTr) {
+#pragma unroll
+        for (int t = 0; t < TJ; ++t) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[t]));
+      }
+      if constexpr (MODE == kGramA) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) fb[t] = scale8_rne(fb[t], xs);
+      }
+#pragma unroll
+      for (int t = 0; t < TJ; ++t) fa[t] = scale8_rne(fa[t], xs);
+    }
+  };
+
   f32x16_t acc[TJ][4];
 #pragma unroll
   for (int a = 0; a < TJ; ++a)
@@ -295,6 +324,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   // half's reads are issued ahead of the other half's 16 MFMAs.
   frags(0, 0, fa0, fb0);
   wait_lgkm<0>();
+  scale_frags(fa0, fb0);
   __builtin_amdgcn_sched_barrier(0);
   frags(0, 1, fa1, fb1);
   __builtin_amdgcn_sched_barrier(0);
@@ -305,6 +335,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     mma(fa0, fb0);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm<0>();  // second-half fragments of unit u
+    scale_frags(fa1, fb1);
     wait_unit<L, NR, RL>(nk, u + 1, pre_st);
     lds_barrier();
     mma_row(fa1, fb1, 0);
@@ -324,6 +355,8 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     if constexpr (TJ > 3) mma_row(fa1, fb1, 3);
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm<0>();  // first-half fragments of unit u + 1
+    scale_frags(fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
     frags(u + 1, 1, fa1, fb1);
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -336,6 +369,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   mma(fa0, fb0);
   __builtin_amdgcn_sched_barrier(0);
   wait_lgkm<0>();
+  scale_frags(fa1, fb1);
   mma(fa1, fb1);
 
   // ---- epilogue ------------------------------------------------------------------
@@ -359,7 +393,8 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
           float y[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float x = bf16_to_f32(half16(rv[e >> 1], e & 1));
+            float x = bf16_to_f32(half16(rv[e >> 1], e & 1));
+            if constexpr (SC) x = bf16_to_f32(pk_bf16(x * xs, 0.f) & 0xffffu);
             const float v = acc[tj][ti][4 * q + e];
             if constexpr (MODE == kApply)  // bf16(B X) + a X, or B X + a X (2-D form)
               y[e] = fmaf(g.beta, x, g.round_once ? v : bf16_to_f32(pk_bf16(v, 0.f) & 0xffffu));
@@ -460,7 +495,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
 
 // NKC: K units known at compile time (16: K = 512, the tile_size 512 case;
 // 0: K from the arguments). NW: waves per workgroup (4 or 8).
-template <int MODE, int NKC, int NW>
+template <int MODE, int NKC, int NW, bool SC>
 __global__ __launch_bounds__(64 * NW, 1) void ns_st_kernel(StArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
   const int nbi = g.M / BT, nbj = g.N / BT;
@@ -495,23 +530,12 @@ __global__ __launch_bounds__(64 * NW, 1) void ns_st_kernel(StArgs g) {
     const int64_t next = item + wper;
     const bool more = next < iend;
     const ItemPos nxt = pos(more ? next : item);
-    const int st = cur.diag ? st_item<MODE, true, NKC, NW>(g, (lds_u8*)lds, cur, pre_st, more, nxt)
-                            : st_item<MODE, false, NKC, NW>(g, (lds_u8*)lds, cur, pre_st, more, nxt);
+    const int st = cur.diag ? st_item<MODE, true, NKC, NW, SC>(g, (lds_u8*)lds, cur, pre_st, more, nxt)
+                            : st_item<MODE, false, NKC, NW, SC>(g, (lds_u8*)lds, cur, pre_st, more, nxt);
     if (!more) break;
     pre_st = st;
     item = next;
     cur = nxt;
-  }
-}
-
-// X0 = bf16(x * inv) in place, 8 elements per thread.
-__global__ __launch_bounds__(NT) void ns_st_scale_kernel(uint16_t* __restrict__ x,
-                                                         const float* __restrict__ inv,
-                                                         int64_t per_tile, int64_t ntiles) {
-  const int64_t nvec = ntiles * per_tile / 8;
-  for (int64_t v = (int64_t)blockIdx.x * NT + threadIdx.x; v < nvec; v += (int64_t)gridDim.x * NT) {
-    u32x4_t* p = reinterpret_cast<u32x4_t*>(x) + v;
-    *p = scale8(*p, inv[(v * 8) / per_tile]);
   }
 }
 
@@ -525,7 +549,7 @@ int num_cus() {
   return n;
 }
 
-template <int MODE>
+template <int MODE, bool SC = false>
 void launch(const StArgs& a, int64_t items, hipStream_t s) {
   const int64_t per_xcd = (items + 7) / 8;
   const int64_t wgs_per_xcd = std::max<int64_t>(1, std::min<int64_t>(num_cus() / 8, per_xcd));
@@ -534,9 +558,9 @@ void launch(const StArgs& a, int64_t items, hipStream_t s) {
   // at K = 256 and 1024 on MI355X, so only that layout is launched.
   constexpr int kNW = 8;
   if (a.K == 16 * BK)
-    hipLaunchKernelGGL((ns_st_kernel<MODE, 16, kNW>), grid, dim3(64 * kNW), 0, s, a);
+    hipLaunchKernelGGL((ns_st_kernel<MODE, 16, kNW, SC>), grid, dim3(64 * kNW), 0, s, a);
   else
-    hipLaunchKernelGGL((ns_st_kernel<MODE, 0, kNW>), grid, dim3(64 * kNW), 0, s, a);
+    hipLaunchKernelGGL((ns_st_kernel<MODE, 0, kNW, SC>), grid, dim3(64 * kNW), 0, s, a);
 }
 
 }  // namespace
@@ -548,7 +572,7 @@ void ns_stream_product(int mode, const uint16_t* P, int64_t p_bs, int ldp, const
                        int M, int N, int K, int64_t ntiles, float alpha, float beta, bool round_once,
                        hipStream_t s) {
   const StArgs g{P, p_bs, ldp, Q, q_bs, ldq, R, r_bs, ldr, C, c_bs, ldc, M, N, K, ntiles, alpha, beta,
-                 round_once ? 1 : 0};
+                 round_once ? 1 : 0, nullptr};
   const int nb = M / BT;
   if (mode == kApply)
     launch<kApply>(g, ntiles * nb * (N / BT), s);
@@ -559,8 +583,8 @@ void ns_stream_product(int mode, const uint16_t* P, int64_t p_bs, int ldp, const
 }
 
 // One sub-batch of `cnt` tiles, `steps` >= 1 iterations, ping-ponging X
-// between x and y (x is scaled in place first); A and B live in the
-// workspace.
+// between x and y; the first iteration's kernels scale the raw x on load
+// (X0 is never written); A and B live in the workspace.
 void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
                     float a, float b, float c, bool round_once, bool fused_ba, uint16_t* wsA, uint16_t* wsB,
                     hipStream_t s) {
@@ -568,23 +592,28 @@ void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int
   const int nb = mp / BT;
   const int64_t gram_items = cnt * (nb * (nb + 1) / 2);
   const int64_t apply_items = cnt * nb * (np / BT);
-  const int64_t nvec = cnt * rect / 8;
-  hipLaunchKernelGGL(ns_st_scale_kernel, dim3((unsigned)std::min<int64_t>((nvec + NT - 1) / NT, 65536)),
-                     dim3(NT), 0, s, x, inv, rect, cnt);
   uint16_t* cur = x;
   uint16_t* nxt = y;
   for (int it = 0; it < steps; ++it) {
-    const StArgs ga{cur, rect, np, cur, rect, np, nullptr, 0, 0, wsA, sq, mp, mp, mp, np, cnt, 1.0f, 0.0f, 0};
-    launch<kGramA>(ga, gram_items, s);
+    const float* xinv = it == 0 ? inv : nullptr;
+    const StArgs ga{cur, rect, np, cur, rect, np, nullptr, 0, 0, wsA, sq, mp, mp, mp, np, cnt, 1.0f, 0.0f, 0, xinv};
+    if (xinv)
+      launch<kGramA, true>(ga, gram_items, s);
+    else
+      launch<kGramA>(ga, gram_items, s);
     if (fused_ba) {  // B stays on chip: ns5_ba.hip
-      ns5_ba_run(wsA, cur, nxt, cnt, a, b, c, round_once, s);
+      ns5_ba_run(wsA, cur, nxt, xinv, cnt, a, b, c, round_once, s);
       std::swap(cur, nxt);
       continue;
     }
-    const StArgs gb{wsA, sq, mp, wsA, sq, mp, wsA, sq, mp, wsB, sq, mp, mp, mp, mp, cnt, c, b, 0};
+    const StArgs gb{wsA, sq, mp, wsA, sq, mp, wsA, sq, mp, wsB, sq, mp, mp, mp, mp, cnt, c, b, 0, nullptr};
     launch<kGramB>(gb, gram_items, s);
-    const StArgs ap{wsB, sq, mp, cur, rect, np, cur, rect, np, nxt, rect, np, mp, np, mp, cnt, 1.0f, a, round_once ? 1 : 0};
-    launch<kApply>(ap, apply_items, s);
+    const StArgs ap{wsB, sq, mp, cur, rect, np, cur, rect, np, nxt, rect, np, mp, np, mp, cnt, 1.0f, a,
+                    round_once ? 1 : 0, xinv};
+    if (xinv)
+      launch<kApply, true>(ap, apply_items, s);
+    else
+      launch<kApply>(ap, apply_items, s);
     std::swap(cur, nxt);
   }
 }

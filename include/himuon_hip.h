@@ -134,8 +134,10 @@ size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np);
  *     X = bf16(bf16(B X) + a * X)
  *
  * x, y: (n_tiles, mp, np) bf16; X ping-pongs between them, so the result is
- * in x when `steps` is even and in y when it is odd (x is overwritten; x and
- * y must not alias). Tiles with mp == 128 and np <= 256 run all iterations
+ * in x when `steps` is even and in y when it is odd (the other buffer's
+ * contents are unspecified afterwards; x and y must not alias). X0 is formed
+ * by the first iteration's kernels as they read x, not by a separate pass.
+ * Tiles with mp == 128 and np <= 256 run all iterations
  * of a tile inside one workgroup's LDS; tiles whose mp and np are multiples
  * of 256 run on persistent 256x256-block kernels; other geometries on
  * 128x128-block kernels. Tiles are processed in sub-batches of `sub_batch`;
