@@ -16,8 +16,9 @@
 //
 //  Stage 1: B_P[i][j] = bf16(c sum_k A[i0+i][k] A[j][k] + b A[i0+i][j]).
 //    Row-side operand A_P (128 x 512 bf16 = 128 KiB) resident in LDS region
-//    R, loaded with direct-to-LDS DMA right after the previous item's last
-//    read of R. Column-side operand: A is exactly symmetric, so A[j][k] =
+//    R, loaded with direct-to-LDS DMA during the previous item's stage 2, a
+//    quarter at a time as soon as every wave has read the B_P columns it
+//    replaces. Column-side operand: A is exactly symmetric, so A[j][k] =
 //    A[k][j] and the wave streams rows k of A restricted to its 128 columns.
 //  Stage 2: X'_P[i][j] = bf16(bf16(sum_k B_P[i][k] X[k][j]) + a X[i0+i][j]).
 //    Row-side operand B_P, written over A_P in R by the stage-1 epilogue;
@@ -38,12 +39,13 @@
 //  through the wave's 8 KiB staging area, the result back through it into
 //  256-byte row stores, and the next item's first ring units loaded.
 //
-// Per item the waves meet at four barriers: A_P landed, A_P reads done, B_P
-// written, B_P reads done (R free for the next item's DMA). Each output
+// Per item the waves meet at barriers: A_P landed, A_P reads done, B_P
+// written, a quarter of B_P read (three times inside stage 2), all of B_P
+// read. Each output
 // element sums its k terms in one fp32 accumulator in ascending k with the
 // same MFMA as the three-kernel path, so results are bit-identical to it.
 //
-// LDS: R (128 KiB, fragment-major, below), then a 8 KiB area per wave (two
+// LDS: R (128 KiB, 8-row blocks, below), then a 8 KiB area per wave (two
 // 4 KiB staging buffers: 16 rows x 256 B, chunk c of row r at c ^ 4 (r % 4),
 // conflict-free for row writes and transposing reads; epilogue: 32 rows x
 // 256 B, chunk c of row r at c ^ (r % 16)).
@@ -97,11 +99,13 @@ struct Unit {
   u32x4_t v[8];
 };
 
-// Region R holds a 128 x 512 panel (A_P, then B_P) fragment-major: fragment
-// (ti, ks) (rows 32 ti .. + 31, k = 16 ks .. + 15) is 1 KiB at (4 ks + ti) KiB,
-// lane l's 16 bytes (row 32 ti + l % 32, k = 16 ks + 8 (l / 32) .. + 7) at
-// 16 l: one lane base plus an immediate per fragment, conflict-free.
-HM_DEV int frag_off(int ti, int ks) { return (4 * ks + ti) * 1024; }
+// Region R holds a 128 x 512 panel (A_P, then B_P) in 1 KiB blocks of 8 rows
+// x 64 k: block (g, m) (rows 8 g .., k = 64 m ..) at (8 g + m) KiB, row r % 8
+// at 128 (r % 8), 16-byte chunk c (k = 64 m + 8 c ..) at position
+// c ^ swz(r). One direct-to-LDS instruction fills a block from 8 rows x 128
+// contiguous bytes; the 16 lanes of a fragment read (rows r .. r + 15, one
+// chunk) hit 16 distinct 16-byte bank groups.
+HM_DEV int r_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // SC (the first iteration): every X value (stage-2 rows, the a X term) is
 // replaced by bf16(x xinv[tile]) before it is used.
@@ -113,8 +117,18 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int l32 = lane & 31, hi = lane >> 5;
   const uint32_t r_base = (uint32_t)(uintptr_t)lds;
-  // lane base of the R fragments (fragment offsets added per k-step)
-  const lds_u8* const Rl0 = lds + 16 * lane;
+  // R row fragments: fragment (ti, ks) of lane l (row 32 ti + l32, chunk
+  // 2 (ks % 4) + hi of block column ks / 4) is at a per-k-step lane base
+  // plus the immediate 32 KiB ti. The chunk term is made opaque per k-step,
+  // so that the four bases are formed where they are used (two VALU
+  // operations) instead of being held through the K loops.
+  const int rl_row = 8192 * (l32 >> 3) + 128 * (l32 & 7);
+  const int rl_sw = hi ^ r_swz(l32);
+  auto rfrag_base = [&](int ks) -> const lds_u8* {
+    int sw = rl_sw;
+    asm volatile("" : "+v"(sw));
+    return lds + rl_row + 16 * ((2 * (ks & 3)) ^ sw) + 1024 * (ks >> 2);
+  };
   lds_u8* const W = lds + R_BYTES + wave * WAREA;
   // Row staging: two 4 KiB buffers (k-steps ks % 2), 16 rows x 256 bytes,
   // 16-byte chunk c of row r at c ^ 4 (r % 4) (conflict-free for the row
@@ -150,17 +164,21 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
 #pragma unroll
     for (int n = 0; n < 8; ++n) load_row(M, row0, d, n);
   };
-  // A_P into R, fragment-major: one 1 KiB fragment per instruction. Call q
-  // (0..3) loads the fragments of k-steps 8 q .. 8 q + 7: wave w takes k-steps
-  // 8 q + 2 w, 8 q + 2 w + 1, every ti (ln, wv: the lane and wave index,
-  // opaque per call so the addresses are formed where they are used).
+  // A_P into R, one block per instruction: lane l lands at row l / 8,
+  // position l % 8 and fetches chunk (l % 8) ^ swz(row). Call q (0..3) loads
+  // block columns m = 2 q, 2 q + 1 (k-steps 8 q .. 8 q + 7); wave w takes
+  // block rows g = 4 w .. 4 w + 3 (ln, wv: the lane and wave index, opaque
+  // per call so the addresses are formed where they are used).
   auto dma_ap = [&](const uint16_t* At, int i0, int q, int ln, int wv) {
-    const uint16_t* src = At + (i0 + (ln & 31)) * T + 8 * (ln >> 5) + 16 * (8 * q + 2 * wv);
-    const uint32_t dst = r_base + frag_off(0, 8 * q + 2 * wv);
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
+    for (int gg = 0; gg < 4; ++gg) {
+      const int g = 4 * wv + gg;
+      const int rr = ln >> 3;  // row within the block
+      const int ch = (ln & 7) ^ rr ^ (gg & 1);
+      const uint16_t* src = At + (i0 + 8 * g + rr) * T + 128 * q + 8 * ch;
 #pragma unroll
-      for (int k = 0; k < 2; ++k) dma16(src + 32 * ti * T + 16 * k, dst + frag_off(ti, k));
+      for (int mm = 0; mm < 2; ++mm) dma16(src + 64 * mm, r_base + 1024 * (8 * g + 2 * q + mm));
+    }
   };
 
   Unit ring[NSLOT];
@@ -189,6 +207,8 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     uint16_t* Yt = g.Y + tile * (int64_t)T * T;
     const int next = item + wper;
     const bool more = next < iend;
+    const uint16_t* const nAt = g.A + ((more ? next : item) >> 2) * (int64_t)T * T;
+    const int ni0 = P * (next & 3);
     float xs = 1.f;
     if constexpr (SC) xs = g.xinv[tile];
 
@@ -217,8 +237,9 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     auto read_frags = [&](int ks, int b, int part) {
       const int buf = 4096 * (ks & 1);
       if (part == 0) {
+        const lds_u8* const rb = rfrag_base(ks);
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) fb[b][ti] = *reinterpret_cast<const lds_u32x4*>(Rl0 + frag_off(ti, ks));
+        for (int ti = 0; ti < 4; ++ti) fb[b][ti] = *reinterpret_cast<const lds_u32x4*>(rb + 32768 * ti);
       } else {
 #pragma unroll
         for (int t2 = 2 * (part - 1); t2 < 2 * (part - 1) + 2; ++t2) {
@@ -272,6 +293,16 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
             load_row(M, row0, dst, 4 * s + tj);
             __builtin_amdgcn_sched_barrier(0);
           }
+          // Stage 2, after k-step 8 q + 7 (q < 3): every wave has consumed
+          // the B_P fragments of k-steps up to 8 q + 7 (block columns 2 q,
+          // 2 q + 1; the reads in flight are of k-step 8 q + 8), so after a
+          // barrier those blocks take the next item's A_P. The fourth quarter
+          // follows the loop.
+          if (xrows && (ks & 7) == 7 && ks + 1 < NKS && more) {
+            asm volatile("s_barrier" ::: "memory");
+            dma_ap(nAt, ni0, ks >> 3, lane_o, wave_o);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
     };
@@ -280,13 +311,16 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     kloop(0);
 
     // ---- stage-1 epilogue: B_P = bf16(c acc + b A_P) over A_P, own columns ----------
-    // element (i = 32 ti + l32, j = 128 w + 32 tj + 8 q + 4 hi + e) is k = j of
-    // fragment (ti, 8 w + 2 tj + q / 2), lane l32 + 32 (q % 2), bytes 8 hi ..:
-    // lane base plus an immediate.
+    // element (i = 32 ti + l32, j = 128 w + 32 tj + 8 q + 4 hi + e): block
+    // (4 ti + l32 / 8, 2 w + tj / 2), row l32 % 8, chunk 4 (tj % 2) + q, bytes
+    // 8 hi ..
     lds_barrier();  // every wave is done reading A_P fragments
     {
-      lds_u8* const ep1 = lds + 32768 * wave + 16 * (lane_o & 31) + 8 * (lane_o >> 5);
-      auto ep1_off = [](int ti, int tj, int q) { return 8192 * tj + 4096 * (q >> 1) + 512 * (q & 1) + 1024 * ti; };
+      const int el = lane_o & 31, esw = r_swz(el);
+      lds_u8* const ep1 = lds + 8192 * (el >> 3) + 2048 * wave + 128 * (el & 7) + 8 * (lane_o >> 5);
+      auto ep1_off = [&](int ti, int tj, int q) {
+        return 32768 * ti + 1024 * (tj >> 1) + 16 * ((4 * (tj & 1) + q) ^ esw);
+      };
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) {
         // all 16 A_P pieces of this row block first, one wait, then B_P over them
@@ -322,16 +356,13 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     kloop(NUNIT);
     // X_P rows i0 + 96 .. i0 + 127 (the fourth X_P unit) into the slot unit 15 freed
     load_rows(Xt, i0 + 96, ring[(2 * NUNIT + AHEAD) % NSLOT]);
-    // All X_P units in before the next A_P's DMA is issued: a wait for an
-    // X_P unit after it would also wait for the DMA (vmcnt retires in order).
+    // All X_P units in before the last quarter of the next A_P's DMA is
+    // issued: a wait for an X_P unit after it would also wait for the DMA
+    // (vmcnt retires in order).
     wait_vm<0>();
     lds_barrier();  // every wave is done reading B_P: R is free
     const int nitem = next;
-    const uint16_t* nAt = g.A + ((more ? nitem : item) >> 2) * (int64_t)T * T;
-    if (more) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) dma_ap(nAt, P * (int)(nitem & 3), q, lane_o, wave_o);
-    }
+    if (more) dma_ap(nAt, ni0, 3, lane_o, wave_o);
 
     // ---- stage-2 epilogue -------------------------------------------------------------
     // X_P unit q (rows 32 q ..) sits in ring[(2 NUNIT + q) % NSLOT] = ring[q].
