@@ -25,6 +25,7 @@ Prints one JSON line. ``--gpus N`` with N > 1 exits: this build runs on one GPU.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -67,13 +68,32 @@ def ns_family(mp: int, np_: int, family: str = "auto") -> str:
 
 PEAK_HBM_GBS = 8000.0
 
-# HBM bytes the NS5 stage moves per step, measured with rocprofv3 --pmc
-# FETCH_SIZE and WRITE_SIZE on this config, each scaled by what the counter
-# reads for this script's 256 MiB device copy (FETCH_SIZE x 1.9995, WRITE_SIZE
-# x 1.0): per 3,465-tile dispatch GramA reads 1.837 GB, GramB 2.738 GB, Apply
-# 4.968 GB, the X0 scaling 1.816 GB, each writing 1.817 GB; 20 + 20 + 20 + 4
-# dispatches per step. Other configs: not measured (null).
-NS5_STAGE_TRAFFIC_BYTES = {"qwen3-4b": 314.44e9}
+# HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE (one pass each) over `bench.py --kernel-only`,
+# each scaled by what the counter reads for the 256 MiB device copy this
+# script runs first (a copy reads and writes exactly 256 MiB). Keyed by
+# (config, kernel) with the sha256 (first 16 hex digits) of the kernel's
+# source files: a figure measured on other sources is not reported.
+KERNEL_TRAFFIC = {
+    # 4096 tiles: FETCH_SIZE 5,047,199 KiB x 1.99970, WRITE_SIZE 2,097,152 KiB x 1.0
+    ("qwen3-4b", "ns_ba_kernel"): (1.2483e+10, "7286bf56a90e560a"),
+    # 65,536 tiles of 128 x 128: FETCH_SIZE 1,050,858 KiB x 1.99969, WRITE_SIZE 2,097,152 KiB x 1.0
+    ("llama3-8b-t128", "ns5_lds_kernel"): (4.2993e+09, "5234145e224f895d"),
+}
+KERNEL_SOURCES = {
+    "ns_ba_kernel": ["ns5_ba.hip", "ns5_kernels.h", "common.h"],
+    "ns5_lds_kernel": ["ns5_lds.hip", "ns5_kernels.h", "common.h"],
+    "ns_st_kernel": ["ns5_stream.hip", "ns5_kernels.h", "common.h"],
+}
+
+
+def sources_digest(kernel: str) -> str:
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES[kernel]:
+        with open(os.path.join(ROOT, "himuon_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
 
 CONFIGS = {
     # name: (layers, [(h, w) per layer], tile_size, param dtype, description)
@@ -146,6 +166,89 @@ def time_ns_stage(opt, reps: int) -> float:
         e1.record(s)
     torch.cuda.synchronize()
     return sum(e0.elapsed_time(e1) for e0, e1 in evs) / reps
+
+
+def _event_loop(fn, reps: int, prep=None) -> float:
+    """Average ms of fn() over reps runs, HIP events around each run on the
+    current stream (the stream the library launches on); prep() runs
+    untimed before each."""
+    s = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    if prep:
+        prep()
+    fn()
+    torch.cuda.synchronize()
+    for e0, e1 in evs:
+        if prep:
+            prep()
+        e0.record(s)
+        fn()
+        e1.record(s)
+    torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in evs) / reps
+
+
+def time_dominant_kernel(opt, reps: int) -> dict:
+    """Per-launch time of the kernel that dominates the NS stage, on one
+    sub-batch of the first group's tiles, from freshly gathered momentum:
+    - 512 x 512 tiles: ns_ba_kernel (himuon_ba_bmm_add: c A A^T + b A and
+      B X + a X fused) on X0 = bf16(x inv) and A = bf16(X0 X0^T); the first
+      product (ns_st_kernel<0>, himuon_xxt) is timed beside it;
+    - other geometries: one himuon_ns5 call on the sub-batch (ns5_lds_kernel
+      for 128-row tiles: all iterations in one launch).
+    Algorithmic FLOPs per launch: 4 m^3 per tile for ns_ba_kernel (2 m^3 for
+    c A A^T, 2 m^2 n for B X with m = n), 2 m^2 n for the Gram kernel, the
+    normative 5 (4 m^2 n + 2 m^3) per tile for a whole NS call."""
+    from himuon_amd import _native as nat
+
+    g = opt._groups[0]
+    grp = g["tiles"]
+    fam = ns_family(grp.mp, grp.np)
+    n = min(g["sub_batch"], grp.n_tiles)
+    m, nn = grp.mp, grp.np
+    x, y, inv = grp.tiles[:n], grp.alt[:n], grp.inv[:n]
+    if fam == "fused":
+        grp.gather()
+        nat.ns5(x, y, inv, n, m, nn, 0, opt._workspace, n)  # X0 = bf16(x inv) in place
+        A = opt._workspace[: n * m * m * 2].view(torch.bfloat16).view(n, m, m)
+        gram_ms = _event_loop(lambda: nat.xxt(x, A, n, m, nn), reps)
+        ba_ms = _event_loop(lambda: nat.ba_bmm_add(A, x, y, n, nat.NS_C, nat.NS_B, nat.NS_A), reps)
+        flops = 4.0 * m**3 * n
+        return {"kernel": "ns_ba_kernel", "family": fam, "launch_tiles": n, "launch_ms": ba_ms,
+                "flops_per_launch": flops, "gram_kernel_launch_ms": gram_ms,
+                "gram_kernel_tflops": 2.0 * m * m * nn * n / (gram_ms * 1e-3) / 1e12}
+    steps = g["steps"]
+    ms = _event_loop(lambda: nat.ns5(x, y, inv, n, m, nn, steps, opt._workspace, n, round_once=grp.round_once),
+                     reps, prep=grp.gather)
+    name = {"lds": "ns5_lds_kernel", "stream": "ns_st_kernel", "small": "ns_gram_kernel/ns_apply_kernel"}[fam]
+    return {"kernel": name, "family": fam, "launch_tiles": n, "launch_ms": ms,
+            "flops_per_launch": float(ns_flops(grp.m, grp.n)) * n}
+
+
+def kernel_roofline(config: str, dk: dict) -> dict:
+    tflops = dk["flops_per_launch"] / (dk["launch_ms"] * 1e-3) / 1e12
+    entry = KERNEL_TRAFFIC.get((config, dk["kernel"]))
+    traffic = None
+    if entry is not None and dk["kernel"] in KERNEL_SOURCES and entry[1] == sources_digest(dk["kernel"]):
+        traffic = entry[0]
+    out = {
+        "kernel": f"{dk['kernel']} ({dk['launch_tiles']} tiles per launch)",
+        "bound": "mfma",
+        "achieved": round(tflops, 1),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "traffic": traffic,
+        "launch_ms": round(dk["launch_ms"], 4),
+        "flops_per_launch": dk["flops_per_launch"],
+    }
+    if traffic:
+        out["traffic_gbs"] = round(traffic / (dk["launch_ms"] * 1e-3) / 1e9, 1)
+        out["intensity_flop_per_byte"] = round(dk["flops_per_launch"] / traffic, 1)
+    if "gram_kernel_launch_ms" in dk:
+        out["gram_kernel_launch_ms"] = round(dk["gram_kernel_launch_ms"], 4)
+        out["gram_kernel_tflops"] = round(dk["gram_kernel_tflops"], 1)
+    return out
 
 
 def time_io_stage(opt, reps: int) -> tuple[float, float]:
@@ -353,6 +456,9 @@ def main():
     ap.add_argument("--no-adamw", action="store_true",
                     help="skip the AdamW fallback timing (Qwen3-4B embedding, fused vs torch ops)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="after the warm-up steps, only time the dominant NS kernel (the command the "
+                         "rocprofv3 counter passes run) and print its roofline")
     ap.add_argument("--reconfigure", type=int, default=None, metavar="T",
                     help="after the timed steps, reconfigure(tile_size=T) and time the eager "
                          "warm-up steps, the recapture step and the replays of the new regime")
@@ -385,6 +491,12 @@ def main():
     for _ in range(warmup):
         opt.step()
     torch.cuda.synchronize()
+    if args.kernel_only:
+        dk = time_dominant_kernel(opt, reps=max(3, args.steps))
+        print(json.dumps({"config": args.config, "roofline": kernel_roofline(args.config, dk),
+                          "sources_digest": sources_digest(dk["kernel"]) if dk["kernel"] in KERNEL_SOURCES
+                          else None}), flush=True)
+        return
 
     s = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
@@ -408,12 +520,12 @@ def main():
     per_step = np.array([marks[k].elapsed_time(marks[k + 1]) for k in range(args.steps)])
 
     ns_ms = time_ns_stage(opt, reps=max(3, args.steps // 2))
+    dk = time_dominant_kernel(opt, reps=max(3, args.steps // 2))
     gather_ms, untile_ms = time_io_stage(opt, reps=max(3, args.steps // 2))
     apply_ms = time_apply(opt, reps=max(3, args.steps // 2))
     flops = algorithmic_flops(opt)
     n_tiles = sum(g["tiles"].n_tiles for g in opt._groups)
     fams = sorted({ns_family(g["tiles"].mp, g["tiles"].np) for g in opt._groups})
-    traffic = NS5_STAGE_TRAFFIC_BYTES.get(args.config) if fams == ["stream"] else None
     n_el = sum(p.numel() for p in params)
     # bytes per element: update (untile writes it, the WD/LR pass reads it), parameter;
     # fused: the untile reads the NS tile and reads and writes the parameter
@@ -458,21 +570,9 @@ def main():
         "apply_ms": round(apply_ms, 3),
         "apply_gbs": None if fused else round((2 * pb + ub) * n_el / (apply_ms * 1e-3) / 1e9, 1),
         "update_dtype": None if fused else str(opt._groups[0]["tiles"].upd_dtype).replace("torch.", ""),
-        "roofline": {
-            "kernel": "; ".join(NS_KERNELS[f] for f in fams),
-            "bound": "mfma",
-            "achieved": round(ns_tflops, 1),
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(ns_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": traffic,
-            "traffic_gbs": round(traffic / (ns_ms * 1e-3) / 1e9, 1) if traffic else None,
-            "traffic_frac_hbm_peak": round(traffic / (ns_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if traffic else None,
-            # measured arithmetic intensity against the ridge point (peak FLOP/s / peak B/s):
-            # below the ridge the measured traffic, not the MFMA rate, bounds the stage
-            "intensity_flop_per_byte": round(flops / traffic, 1) if traffic else None,
-            "ridge_flop_per_byte": round(PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9), 1),
-        },
+        "ns5_stage_kernels": "; ".join(NS_KERNELS[f] for f in fams),
+        # the dominant kernel, one launch on one sub-batch (HIP events)
+        "roofline": kernel_roofline(args.config, dk),
     }
     if args.reconfigure:
         out["reconfigure"] = time_reconfigure(opt, args.reconfigure, args.steps)

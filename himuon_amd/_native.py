@@ -19,7 +19,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libhimuon_hip.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 NS_ALIGN = 128
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -127,6 +127,8 @@ _SIGNATURES = {
     "himuon_xxt": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_void_p]),
     "himuon_ba_plus_caa": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_float, c_float, c_int, c_void_p]),
     "himuon_bmm_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_int, c_void_p]),
+    "himuon_ba_bmm_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_float, c_float,
+                                  c_int, c_void_p]),
     "himuon_untile": (
         c_int,
         [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p],
@@ -331,6 +333,13 @@ def ba_plus_caa(a, out, batch, M, alpha, beta, family=None):
 def bmm_add(b, x, out, batch, M, N, a, round_once=False, family=None):
     _check(load().himuon_bmm_add(b.data_ptr(), x.data_ptr(), out.data_ptr(), batch, M, N, a,
                                  _stage_flags(family, round_once), _stream()), "himuon_bmm_add")
+
+
+def ba_bmm_add(a, x, out, batch, alpha, beta, gamma, round_once=False):
+    """out = bf16(bf16(B X) + gamma X), B = bf16(alpha A A^T + beta A) kept on
+    chip (512 x 512 tiles; bf16(B X + gamma X) with round_once)."""
+    _check(load().himuon_ba_bmm_add(a.data_ptr(), x.data_ptr(), out.data_ptr(), batch, 512, 512, alpha, beta, gamma,
+                                    NS_ROUND_ONCE if round_once else 0, _stream()), "himuon_ba_bmm_add")
 
 
 def untile(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtype, tiles):

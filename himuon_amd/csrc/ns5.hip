@@ -439,3 +439,17 @@ extern "C" int himuon_bmm_add(const uint16_t* b, const uint16_t* x, uint16_t* ou
   }
   return (int)hipGetLastError();
 }
+
+// ba_plus_cAA followed by fused_bmm_add as one kernel (ns5_ba.hip): B never
+// leaves the CU. 512 x 512 only (the fused kernel's tile).
+extern "C" int himuon_ba_bmm_add(const uint16_t* a, const uint16_t* x, uint16_t* out, int64_t batch, int M,
+                                 int N, float alpha, float beta, float gamma, int flags, void* stream) {
+  if (!a || !x || !out || out == x || out == a || batch < 0 || !ns5_ba_supported(M, N) ||
+      (flags & ~HIMUON_NS_ROUND_ONCE))
+    return HIMUON_EINVAL;
+  if (batch == 0) return 0;
+  if (batch > (int64_t(1) << 29)) return HIMUON_EINVAL;  // 32-bit work-item indices
+  ns5_ba_run(a, x, out, nullptr, batch, gamma, beta, alpha, (flags & HIMUON_NS_ROUND_ONCE) != 0,
+             static_cast<hipStream_t>(stream));
+  return (int)hipGetLastError();
+}

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HIMUON_ABI_VERSION 2
+#define HIMUON_ABI_VERSION 3
 
 /* Element type codes for gradients / momentum / updates. */
 #define HIMUON_DTYPE_F32 0
@@ -138,9 +138,11 @@ size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np);
  * contents are unspecified afterwards; x and y must not alias). X0 is formed
  * by the first iteration's kernels as they read x, not by a separate pass.
  * Tiles with mp == 128 and np <= 256 run all iterations
- * of a tile inside one workgroup's LDS; tiles whose mp and np are multiples
- * of 256 run on persistent 256x256-block kernels; other geometries on
- * 128x128-block kernels. Tiles are processed in sub-batches of `sub_batch`;
+ * of a tile inside one workgroup's LDS; 512 x 512 tiles run the first
+ * product on a persistent 256x256-block kernel and the other two fused
+ * (himuon_ba_bmm_add's kernel); other tiles whose mp and np are multiples of
+ * 256 run the three products on persistent 256x256-block kernels; other
+ * geometries on 128x128-block kernels. Tiles are processed in sub-batches of `sub_batch`;
  * the workspace must hold himuon_ns5_workspace_bytes(sub_batch, mp, np)
  * bytes whenever steps > 0.
  */
@@ -196,6 +198,20 @@ int himuon_ba_plus_caa(const uint16_t* a, uint16_t* out, int64_t batch, int M,
                        float alpha, float beta, int flags, void* stream);
 int himuon_bmm_add(const uint16_t* b, const uint16_t* x, uint16_t* out,
                    int64_t batch, int M, int N, float a, int flags, void* stream);
+
+/*
+ * The second and third products fused, with B kept on chip (the kernel the
+ * optimizer runs for 512 x 512 tiles):
+ *     out = bf16(bf16(B X) + gamma * X),  B = bf16(alpha * (A A^T) + beta * A)
+ * (bf16(B X + gamma * X) with HIMUON_NS_ROUND_ONCE). No single reference
+ * counterpart: it equals ba_plus_cAA (ba_plus_cAA.py:90-120) followed by
+ * fused_bmm_add (fused_bmm_add.py:98-135), bit for bit. A: (batch, 512, 512)
+ * bf16, exactly symmetric (an XXT output); X, out: (batch, 512, 512) bf16;
+ * M == N == 512, batch <= 2^29; `flags` takes only HIMUON_NS_ROUND_ONCE.
+ */
+int himuon_ba_bmm_add(const uint16_t* a, const uint16_t* x, uint16_t* out,
+                      int64_t batch, int M, int N, float alpha, float beta,
+                      float gamma, int flags, void* stream);
 
 /*
  * Untile/scatter: for every element of every parameter,

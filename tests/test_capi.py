@@ -160,6 +160,13 @@ def test_ns5_ex_and_stage_argument_errors(lib):
     assert lib.himuon_bmm_add(8, 16, 24, 1, 256, 200, 1.0, 0, z) == -22
     assert lib.himuon_bmm_add(8, 16, 24, 1, 256, 256, 1.0, 0x20, z) == -22
     assert lib.himuon_bmm_add(8, 16, 24, 0, 256, 256, 1.0, 0x10, z) == 0
+    # the fused second and third products: 512 x 512 only, no aliasing, round-once only
+    assert lib.himuon_ba_bmm_add(8, 16, 24, 1, 256, 256, 1.0, 1.0, 1.0, 0, z) == -22
+    assert lib.himuon_ba_bmm_add(8, 16, 24, 1, 512, 1024, 1.0, 1.0, 1.0, 0, z) == -22
+    assert lib.himuon_ba_bmm_add(8, 16, 16, 1, 512, 512, 1.0, 1.0, 1.0, 0, z) == -22
+    assert lib.himuon_ba_bmm_add(8, 16, 24, 1, 512, 512, 1.0, 1.0, 1.0, 1, z) == -22
+    assert lib.himuon_ba_bmm_add(8, 16, 24, (1 << 29) + 1, 512, 512, 1.0, 1.0, 1.0, 0, z) == -22
+    assert lib.himuon_ba_bmm_add(8, 16, 24, 0, 512, 512, 1.0, 1.0, 1.0, 0x10, z) == 0
 
 
 def test_geometry_helpers():

@@ -7,6 +7,7 @@ same GPU.
 * ba_plus_cAA:    B = bf16(c A A^T + b A)       vs torch.baddbmm(A, A, A^T, beta=b, alpha=c)
 * fused_bmm_add:  X' = bf16(bf16(B X) + a X)    vs torch.add(torch.bmm(B, X), X, alpha=a)
 * 2-D form:       X' = bf16(B X + a X)          vs torch.addmm(X, B, X, beta=a)
+* ba_bmm_add:     the last two fused (B on chip) vs the two stages, bit for bit
 
 The kernels accumulate each output in one fp32 register over k in ascending
 order with the same MFMA shape as torch's bf16 GEMMs on this GPU, so the
@@ -116,6 +117,26 @@ def test_bmm_add_2d_form_matches_torch_addmm(batch, M, N, family):
     # and it is not the batched form
     twice = torch.add(torch.bmm(Bm, X), X, alpha=A_)
     assert not torch.equal(out, twice)
+
+
+@pytest.mark.parametrize("round_once", [False, True])
+def test_fused_ba_bmm_add_equals_the_two_stages(round_once):
+    """himuon_ba_bmm_add (B kept on chip) == ba_plus_cAA then fused_bmm_add,
+    bit for bit, and == torch's baddbmm then bmm + add."""
+    print(f"[ba_bmm_add] round_once={round_once}", flush=True)
+    n = 6
+    X = _normalised(_rand((n, 512, 512), seed=17))
+    A = _sym(X)
+    Bm = torch.empty_like(A)
+    nat.ba_plus_caa(A, Bm, n, 512, C_, B_)
+    two = torch.empty_like(X)
+    nat.bmm_add(Bm, X, two, n, 512, 512, A_, round_once=round_once)
+    fused = torch.full_like(X, float("nan"))
+    nat.ba_bmm_add(A, X, fused, n, C_, B_, A_, round_once=round_once)
+    assert torch.equal(fused, two)
+    if not round_once:
+        ref = torch.add(torch.bmm(torch.baddbmm(A, A, _t(A), beta=B_, alpha=C_), X), X, alpha=A_)
+        assert torch.equal(fused, ref)
 
 
 def test_stage_products_compose_to_ns_iteration():
