@@ -25,7 +25,9 @@
 // ahead of the MFMAs that need them (7 % faster than 2- and 4-fold unrolling).
 //
 // LDS rows hold 16-byte chunks; chunk ch of row r sits at position
-// ch ^ (r & 15), so 16 consecutive rows of one chunk cover all 64 banks.
+// ch ^ s(r), s(r) = 4 (r % 4) + (r / 4) % 4: 16 consecutive rows of one chunk
+// (fragment reads) and 4 consecutive rows of 4 consecutive chunks
+// (transposing reads, mirrored Gram stores) both cover all 16 bank groups.
 // np = 128: 64 KiB per workgroup, two workgroups per CU; np = 256: 96 KiB.
 #include "ns5_kernels.h"
 
@@ -39,7 +41,8 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 typedef __attribute__((address_space(3))) u32x4_t lds_u32x4;
 
 HM_DEV uint32_t lds_pos(int r, int ch, int chunks) {
-  return (uint32_t)(r * chunks + (ch ^ (r & 15))) * 16u;
+  const int sw = ((r & 3) << 2) | ((r >> 2) & 3);
+  return (uint32_t)(r * chunks + (ch ^ sw)) * 16u;
 }
 
 // Transposing read: 4 bf16 of the 8-byte row segment at `off`, redistributed
