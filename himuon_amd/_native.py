@@ -129,6 +129,8 @@ _SIGNATURES = {
     "himuon_bmm_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_int, c_void_p]),
     "himuon_ba_bmm_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_float, c_float,
                                   c_int, c_void_p]),
+    "himuon_ns5_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_float, c_float,
+                                   c_float, c_int, c_void_p]),
     "himuon_untile": (
         c_int,
         [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p],

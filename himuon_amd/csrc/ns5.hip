@@ -19,6 +19,8 @@
 // LDS with register prefetch of the next K slab. Blocks are mapped to XCDs so
 // all blocks of one NS tile share an L2.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "ns5_kernels.h"
 
@@ -362,6 +364,65 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
     if (e != hipSuccess) return (int)e;
   }
   return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free NS5: the A/B workspace is a file-scope device array (one
+// copy per GPU, held until the process ends). Its device address is looked
+// up once per device with that device current; host code uses only that
+// address, never the array's name (a host-side stand-in).
+// ---------------------------------------------------------------------------
+namespace {
+__device__ __align__(256) uint8_t scratch[HIMUON_NS_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_dev[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of this device's `scratch`, or nullptr (err set).
+void* scratch_address(int* err) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *err = (int)e;
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = HIMUON_EINVAL;
+    return nullptr;
+  }
+  void* p = g_scratch_dev[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  p = g_scratch_dev[dev].load(std::memory_order_relaxed);
+  if (!p) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *err = e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+      return nullptr;
+    }
+    g_scratch_dev[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+}  // namespace
+
+extern "C" int himuon_ns5_noalloc(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp,
+                                  int np, int steps, float a, float b, float c, int flags, void* stream) {
+  if (!x || !y || x == y || !inv || n_tiles < 0 || steps < 0 || mp <= 0 || np <= 0 || mp > np ||
+      mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN)
+    return HIMUON_EINVAL;
+  const size_t per_tile = himuon_ns5_workspace_bytes(1, mp, np);
+  if (per_tile > HIMUON_NS_SCRATCH_BYTES) return HIMUON_ENOSPC;  // one tile's A and B do not fit
+  if (n_tiles == 0) return 0;
+  if (steps == 0)  // no workspace needed
+    return himuon_ns5_ex(x, y, inv, n_tiles, mp, np, 0, a, b, c, nullptr, 0, n_tiles, flags, stream);
+  int err = 0;
+  void* ws = scratch_address(&err);
+  if (!ws) return err;
+  const int64_t sub_batch = (int64_t)(HIMUON_NS_SCRATCH_BYTES / per_tile);
+  return himuon_ns5_ex(x, y, inv, n_tiles, mp, np, steps, a, b, c, ws, HIMUON_NS_SCRATCH_BYTES, sub_batch, flags,
+                       stream);
 }
 
 extern "C" int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp,

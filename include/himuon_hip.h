@@ -214,6 +214,27 @@ int himuon_ba_bmm_add(const uint16_t* a, const uint16_t* x, uint16_t* out,
                       float gamma, int flags, void* stream);
 
 /*
+ * himuon_ns5_ex without a workspace argument, for callers that cannot
+ * allocate (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference. It allocates nothing:
+ * the A/B intermediates live in a device array of HIMUON_NS_SCRATCH_BYTES
+ * inside the library, one per GPU, held until the process ends, and the tiles
+ * are processed in sub-batches of HIMUON_NS_SCRATCH_BYTES /
+ * himuon_ns5_workspace_bytes(1, mp, np). Returns HIMUON_ENOSPC when one
+ * tile's workspace exceeds HIMUON_NS_SCRATCH_BYTES (mp above 4096). Results
+ * are identical to himuon_ns5_ex's. Every call on one GPU uses that GPU's
+ * array: calls that overlap on one GPU (other streams or host threads) race
+ * and must be serialised by the caller; nothing in the array needs to start
+ * at zero. The array's device address is looked up on the first call on each
+ * device (the one exception to "no mutable global state": a per-device cache
+ * of that address).
+ */
+#define HIMUON_NS_SCRATCH_BYTES ((size_t)64 << 20)
+int himuon_ns5_noalloc(uint16_t* x, uint16_t* y, const float* inv,
+                       int64_t n_tiles, int mp, int np, int steps, float a,
+                       float b, float c, int flags, void* stream);
+
+/*
  * Untile/scatter: for every element of every parameter,
  *     update[row, col] = round_dtype(upd_scale * float(NS tile value))
  * reading the NS tile position of (row, col) (transposed back when
