@@ -375,6 +375,130 @@ def time_reconfigure(opt, tile: int, steps: int) -> dict:
     }
 
 
+# The reference's NS microbenchmark points (microbench/experiments/
+# exp_ns_kernel_microbench.py:50,279: T = 128, B = 32 / 128 / 512 / 2048; its
+# fused ns5_smem kernel's times read off microbench/plots/ns_kernel_microbench.png,
+# unstated NVIDIA hardware) and its rectangular sweep
+# (exp_ns5_rect_bench.py:83-103,171: M <= N from DIMS, M N + 2 M^2 <= 49152,
+# B = 2^21 // (M N)).
+NS_MICRO_B = {"ns-t128-b32": 32, "ns-t128-b128": 128, "ns-t128-b512": 512, "ns-t128-b2048": 2048}
+NS_MICRO_REF_MS = {32: 0.14, 128: 0.20, 512: 0.46, 2048: 1.55}
+RECT_DIMS = [16, 32, 64, 128, 256, 512, 1024, 2048]
+
+
+def rect_shapes() -> list[tuple[int, int]]:
+    return [(m, n) for m in RECT_DIMS for n in RECT_DIMS if n >= m and m * n + 2 * m * m <= 49152]
+
+
+def ns_micro(B: int, reps: int, warmup: int, T: int = 128) -> dict:
+    """NS5 on B random T x T tiles per call, as the reference's microbenchmark
+    measures it: input torch.randn(B, T, T) bf16 with seed 42
+    (exp_ns_kernel_microbench.py:121-123), a call = the Frobenius normaliser
+    (himuon_tile_scale's formula, 1 / (||x|| + eps), here one torch reduction)
+    + himuon_ns5 (all 5 iterations); median of `reps` calls with HIP events
+    around each, after `warmup` calls. Each call starts from the same input
+    (the NS runs from x into the ping-pong buffer; the input buffer is
+    refreshed untimed)."""
+    from himuon_amd import _native as nat
+
+    torch.manual_seed(42)
+    x0 = torch.randn(B, T, T, device="cuda", dtype=torch.bfloat16)
+    x = x0.clone()
+    y = torch.empty_like(x)
+    inv = torch.empty(B, device="cuda", dtype=torch.float32)
+    ws = torch.empty(max(1, nat.ns5_workspace_bytes(B, T, T)), device="cuda", dtype=torch.uint8)
+
+    def norm():
+        torch.reciprocal(x.float().flatten(1).norm(dim=1).add_(1e-7), out=inv)
+
+    def ns():
+        nat.ns5(x, y, inv, B, T, T, 5, ws, B)
+
+    s = torch.cuda.current_stream()
+    t_call, t_ns = [], []
+    for k in range(warmup + reps):
+        x.copy_(x0)
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record(s)
+        norm()
+        e[1].record(s)
+        ns()
+        e[2].record(s)
+        e[2].synchronize()
+        if k >= warmup:
+            t_call.append(e[0].elapsed_time(e[2]))
+            t_ns.append(e[1].elapsed_time(e[2]))
+    ms, ns_ms = float(np.median(t_call)), float(np.median(t_ns))
+    flops = 30.0 * T**3 * B
+    return {"B": B, "T": T, "ms": ms, "ns5_ms": ns_ms, "tflops": flops / (ms * 1e-3) / 1e12,
+            "ns5_tflops": flops / (ns_ms * 1e-3) / 1e12, "family": ns_family(T, T)}
+
+
+def ns_rect(reps: int, warmup: int, total_elements: int = 1 << 21) -> list[dict]:
+    """The reference's rectangular sweep: for each admitted (M, N), B =
+    total // (M N) random tiles zero-padded into the library's (mp, np)
+    buffer (multiples of 128), the NS5 call timed as in ns_micro (normaliser
+    untimed here: the reference's throughput column counts the NS call).
+    Reported: median ms, the reference's bytes metric (B M N 2 bytes / time)
+    and algorithmic TFLOP/s on the unpadded shape, 5 (4 M^2 N + 2 M^3)."""
+    from himuon_amd import _native as nat
+
+    out = []
+    for m, n in rect_shapes():
+        B = max(1, total_elements // (m * n))
+        mp, np_ = -(-m // 128) * 128, -(-n // 128) * 128
+        torch.manual_seed(42)
+        x0 = torch.zeros(B, mp, np_, device="cuda", dtype=torch.bfloat16)
+        x0[:, :m, :n] = torch.randn(B, m, n, device="cuda", dtype=torch.bfloat16)
+        inv = torch.reciprocal(x0.float().flatten(1).norm(dim=1).add_(1e-7))
+        x, y = x0.clone(), torch.empty_like(x0)
+        ws = torch.empty(max(1, nat.ns5_workspace_bytes(B, mp, np_)), device="cuda", dtype=torch.uint8)
+        s = torch.cuda.current_stream()
+        ts = []
+        for k in range(warmup + reps):
+            x.copy_(x0)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            nat.ns5(x, y, inv, B, mp, np_, 5, ws, B)
+            e1.record(s)
+            e1.synchronize()
+            if k >= warmup:
+                ts.append(e0.elapsed_time(e1))
+        ms = float(np.median(ts))
+        out.append({"M": m, "N": n, "B": B, "mp": mp, "np": np_, "family": ns_family(mp, np_), "ms": round(ms, 4),
+                    "GBps": round(B * m * n * 2 / (ms * 1e-3) / 1e9, 1),
+                    "tflops": round(ns_flops(m, n) * B / (ms * 1e-3) / 1e12, 2)})
+        del x0, x, y, ws
+    return out
+
+
+def ns_micro_line(args) -> dict:
+    """The JSON line of an NS microbenchmark config."""
+    warmup = max(args.warmup, 2)
+    if args.config == "ns-rect":
+        rows = ns_rect(args.steps, warmup)
+        return {"metric": "NS5 time per call (ms) over the reference's (M, N) tile-shape sweep",
+                "value": round(sum(r["ms"] for r in rows), 4), "unit": "ms (sum over shapes)", "n_gpus": 1,
+                "steps": args.steps, "warmup": warmup, "higher_is_better": False, "scaling": "strong",
+                "vs_baseline": None, "dtype": "bf16",
+                "data": "synthetic: torch.randn tiles, seed 42, zero-padded to multiples of 128",
+                "config": {"workload": "ns-rect", "total_elements": 1 << 21, "shapes": len(rows)}, "shapes": rows}
+    B = NS_MICRO_B[args.config]
+    r = ns_micro(B, args.steps, warmup)
+    ref = NS_MICRO_REF_MS[B]
+    return {"metric": "NS5 time per call (ms), T = 128, B tiles (normaliser + 5 iterations)",
+            "value": round(r["ms"], 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": warmup,
+            "ms_per_step": round(r["ms"], 4), "higher_is_better": False, "scaling": "strong",
+            "vs_baseline": round(r["ms"] / ref, 4), "dtype": "bf16",
+            "data": "synthetic: torch.randn(B, 128, 128) bf16, seed 42 (exp_ns_kernel_microbench.py:121-123)",
+            "config": {"workload": args.config, "T": 128, "B": B, "kernel_family": r["family"]},
+            "tflops": round(r["tflops"], 1), "frac_peak": round(r["tflops"] / PEAK_BF16_TFLOPS, 4),
+            "ns5_only_ms": round(r["ns5_ms"], 4), "ns5_only_tflops": round(r["ns5_tflops"], 1),
+            "reference_figure_ms": ref,
+            "reference_figure_note": "the reference's fused ns5_smem kernel, read off ns_kernel_microbench.png "
+                                     "(log axis, unstated NVIDIA GPU); vs_baseline = value / that time"}
+
+
 def _cpu_model() -> tuple[str, bool]:
     """Full CPU model string (lscpu's, else /proc/cpuinfo's) and whether the
     host has native bf16 (AVX512-BF16 or AMX-BF16)."""
@@ -468,7 +592,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS) + sorted(NS_MICRO_B) + ["ns-rect"],
+                    help="a parameter-set config (the HiMuon step), or an NS microbenchmark of the reference's: "
+                         "ns-t128-b{32,128,512,2048} (NS5 per call on B tiles of 128x128) or ns-rect "
+                         "(its rectangular tile-shape sweep)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-adamw", action="store_true",
                     help="skip the AdamW fallback timing (Qwen3-4B embedding, fused vs torch ops)")
@@ -494,6 +621,9 @@ def main():
     from himuon_amd.optimizers.himuon import HiMuon
 
     load()
+    if args.config in NS_MICRO_B or args.config == "ns-rect":
+        print(json.dumps(ns_micro_line(args)), flush=True)
+        return
     # A 256 MiB device copy of known size: under `rocprofv3 --pmc` its
     # FETCH_SIZE / WRITE_SIZE readings calibrate those counters (a plain copy
     # reads and writes exactly 256 MiB), so kernel traffic can be scaled.

@@ -55,3 +55,13 @@ def test_cpu_baseline_times_a_whole_layer_and_extrapolates():
     assert "one full layer" in r["sample"] and "x3 extrapolated" in r["unit"]
     assert abs(r["value"] - 3 * r["layer_ms"]) <= 0.2
     assert r["cpu"]
+
+
+def test_reference_microbenchmark_points():
+    # exp_ns5_rect_bench.py:83-103: M <= N from DIMS with M N + 2 M^2 <= 49152 -> 19 shapes
+    shapes = bench.rect_shapes()
+    assert len(shapes) == 19 and (128, 128) in shapes and (16, 2048) in shapes and (64, 1024) not in shapes
+    assert all(m <= n and m * n + 2 * m * m <= 49152 for m, n in shapes)
+    # exp_ns_kernel_microbench.py:279: B = 32, 128, 512, 2048 at T = 128
+    assert sorted(bench.NS_MICRO_B.values()) == [32, 128, 512, 2048]
+    assert set(bench.NS_MICRO_REF_MS) == set(bench.NS_MICRO_B.values())
