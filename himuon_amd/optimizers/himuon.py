@@ -18,7 +18,11 @@ math per matrix is unchanged.
 
 There is no CPU path: ``step()`` on non-HIP tensors raises, as the
 reference's does without its GPU kernels (triton_kernels/__init__.py:8-19).
-FSDP/DTensor parameters (himuon.py:419-457, 894-1020) are out of scope.
+FSDP bank parameters (DTensor muon parameters whose rank-local shard is a
+3-D bank (N_local, H, W), himuon.py:419-457, 894-1020) take the per-bank
+path: each bank's N_local matrices are tiled separately (padded per matrix),
+NS runs on all of the bank's tiles in one call, and WD/LR is applied to the
+local shard in place; nothing crosses ranks, so no collective runs.
 """
 
 from __future__ import annotations
@@ -172,12 +176,16 @@ class HiMuon(Optimizer):
         self._adamw_tables = None
         self._adamw_sig = None
 
+    def _local(self, t: torch.Tensor) -> torch.Tensor:
+        """The rank-local tensor of a DTensor (shares its storage), else t."""
+        return t.to_local() if self._is_dtensor(t) else t
+
     def _storage_sig(self) -> tuple:
         """Which parameters have a grad, and where each such parameter's and
-        grad's storage lives. The plan, the device descriptor tables and a
-        captured graph all hold these pointers."""
+        grad's storage lives (the local shard's, for DTensors). The plan, the
+        device descriptor tables and a captured graph all hold these pointers."""
         return tuple(
-            (id(p), p.data_ptr(), p.grad.data_ptr())
+            (id(p), self._local(p).data_ptr(), self._local(p.grad).data_ptr())
             for g in self.param_groups
             for p in g["params"]
             if p.grad is not None
@@ -481,9 +489,12 @@ class HiMuon(Optimizer):
     # -- Device state -----------------------------------------------------------
 
     def _momentum_buffer(self, p):
+        """The parameter's momentum buffer (for a DTensor bank, a plain tensor
+        shaped like the local grad shard, as the reference's per-bank path
+        keeps it: himuon.py:350-357 called on the local grad, :906)."""
         st = self.state[p]
         if "momentum_buffer" not in st:
-            st["momentum_buffer"] = torch.zeros_like(p.grad)
+            st["momentum_buffer"] = torch.zeros_like(self._local(p.grad))
         return st["momentum_buffer"]
 
     def _build_groups(self, plan: list[dict]) -> list[dict]:
@@ -570,18 +581,104 @@ class HiMuon(Optimizer):
                     "full": True,
                 }
             )
-        # One NS workspace shared by all groups, sized for the largest need.
+        self._size_workspace(out)
+        return out
+
+    def _bank_sources(self, p, group):
+        """Per-matrix (grads, momentum buffers, mus, nesterovs) of a bank
+        parameter's local shard: 2-D views of the (N, H, W) grad and buffer."""
+        gl = self._local(p.grad)
+        buf = self._momentum_buffer(p)
+        n = gl.shape[0]
+        return [gl[i] for i in range(n)], [buf[i] for i in range(n)], [group["momentum"]] * n, [group["nesterov"]] * n
+
+    def _build_bank_groups(self) -> list[dict]:
+        """FSDP per-bank path (himuon.py:894-964): one tile group per bank
+        parameter, over the N matrices of its local (N, H, W) shard. Each matrix
+        is tiled and padded on its own (himuon.py:920-936); when the tile covers
+        a whole matrix the bank runs NS on (N, H, W) directly with block (H, W)
+        (:912-918). The untile applies WD/LR to the local shard in place. NS is
+        the batched form (newton_schulz on a 3-D input): its third product
+        rounds B X before adding a X."""
+        group_to_idx = {id(g): i for i, g in enumerate(self.param_groups)}
+        out = []
+        for group in self.param_groups:
+            if not group["use_muon"]:
+                continue
+            gi = group_to_idx[id(group)]
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                if not self._is_dtensor(p):
+                    raise RuntimeError(
+                        "HiMuon FSDP path: muon param group contains a non-DTensor param. Mixed "
+                        "DTensor/non-DTensor muon params are not supported. Wrap all muon-eligible "
+                        "params with the same FSDP scheme."
+                    )
+                gl = self._local(p.grad)
+                if gl.ndim != 3:
+                    raise RuntimeError(
+                        f"HiMuon FSDP per-bank path requires bank-wrapped 3D muon params; got local "
+                        f"ndim={gl.ndim} (shape {tuple(gl.shape)}). Call wrap_with_banks() before fully_shard()."
+                    )
+                n, h, w = gl.shape
+                tile_h, tile_w = group["tile_size"]
+                block = (h, w) if (tile_h >= h and tile_w >= w) else (tile_h, tile_w)
+                pl = self._local(p)
+                slices = [pl[i] for i in range(n)]
+                grads, moms, mus, nesterovs = self._bank_sources(p, group)
+                fuse = (
+                    self._fuse_untile and pl.dtype in nat.DTYPE_CODES
+                    and (pl.dtype != torch.float16 or gl.dtype != torch.float32)
+                    and pl.is_cuda and pl.is_contiguous() and gi < nat.APPLY_MAX_GROUPS
+                )
+                grp = TileGroup(
+                    params=slices,
+                    grads=grads,
+                    moms=moms,
+                    tile_h=block[0],
+                    tile_w=block[1],
+                    upd_scales=[self.adjust_lr_for_muon(1.0, block)] * n,
+                    mus=mus,
+                    nesterovs=nesterovs,
+                    device=gl.device,
+                    dtype=gl.dtype,
+                    upd_dtype=update_dtype(slices, gl.dtype),
+                    apply_groups=[gi] * n if fuse else None,
+                )
+                out.append(
+                    {
+                        "tiles": grp,
+                        "entries": [(sl, group) for sl in slices],
+                        "group_idx": [gi] * n,
+                        "steps": group["ns_steps"],
+                        "chunks": [grp.n_tiles],
+                        "full": False,
+                        "bank": p,
+                    }
+                )
+        self._size_workspace(out)
+        return out
+
+    def _size_workspace(self, groups: list[dict]) -> None:
+        """One NS workspace shared by all groups, sized for the largest need."""
         need = 1
-        for g in out:
+        for g in groups:
             grp = g["tiles"]
             g["sub_batch"] = grp.default_sub_batch()
             need = max(need, grp.workspace_bytes(g["sub_batch"]))
-        device = out[0]["tiles"].device if out else None
+        device = groups[0]["tiles"].device if groups else None
         if device is not None and (self._workspace is None or self._workspace.numel() < need):
             self._workspace = torch.empty(need, device=device, dtype=torch.uint8)
-        return out
 
     def _ensure_device_state(self):
+        if self._has_dtensor_muon():  # FSDP per-bank path: no cross-layer plan
+            if self._groups is None:
+                self._groups = self._build_bank_groups()
+            else:
+                for g in self._groups:
+                    g["tiles"].bind(*self._bank_sources(g["bank"], g["entries"][0][1]))
+            return self._groups
         if self._cached_plan is None:
             self._cached_plan = self._plan_buckets()
             self._groups = None
@@ -653,11 +750,13 @@ class HiMuon(Optimizer):
         """Momentum -> tile -> NS5 -> untile for every muon param (HIP), then the
         AdamW groups (torch), with WD/LR applied eagerly or deferred to after
         graph replay."""
-        if self._has_dtensor_muon():
-            raise NotImplementedError("HiMuon (HIP path) runs on one GPU; FSDP/DTensor parameters are not supported")
         groups = self._ensure_device_state()
         stats = self._run_groups(groups) if groups else {"ns_gpu_ms": 0.0, "ns_launches": 0, "total_B": 0}
         self._step_adamw_groups()
+        if groups and "bank" in groups[0]:
+            # the FSDP path's stats (himuon.py:1013-1018): one NS launch per bank
+            self._last_step_stats = {"ns_gpu_ms": 0.0, "ns_launches": len(groups), "total_B": 0, "avg_batch": 0.0}
+            return
         n = stats["ns_launches"]
         self._last_step_stats = {
             "ns_gpu_ms": float(stats["ns_gpu_ms"]),
