@@ -37,6 +37,7 @@ Functions and the reference lines they restate:
                         op rounds to bf16)
   lr_scale              himuon.py:181-186
   fma32 / round_to      correctly rounded fp32 fma; cast to a param dtype
+  apply_update_eager    the reference's eager WD/LR form (himuon.py:342-348)
   apply_update          WD/LR of himuon.py:215-228 / 333-348 as torch's GPU
                         kernels evaluate p.mul_(1-lr*wd) then p.add_(u,
                         alpha=-lr): u rounded to the param dtype, then one
@@ -414,6 +415,22 @@ def apply_update(p, update, lr: float, wd: float, dtype: str = "float32",
         exact = np.float64(F32(-lr)) * u.astype(np.float64) + p.astype(np.float64)
         return exact.astype(np.float16).astype(F32)
     return round_to(fma32(F32(-lr), u, p), dtype)
+
+
+def apply_update_eager(p, ns_out, lr: float, wd: float, scale: float, dtype: str = "float32") -> np.ndarray:
+    """The reference's eager WD/LR form (himuon.py:342-348): the update is the
+    unscaled NS output and the lr-adjust scale rides in the alpha,
+    p.mul_(1 - lr*wd); p.add_(u, alpha=-lr*scale) (alpha formed in double,
+    then fp32). This build always applies the graph form (update scaled
+    first, alpha = -lr: apply_update), which for bf16 parameters rounds the
+    scaled update to bf16 before the add, as the reference's graph path does;
+    the two differ by at most that rounding (2^-8 of lr |u s|) plus one unit
+    in the last place (bound pinned in tests/test_oracle.py)."""
+    p = np.asarray(p, dtype=F32)
+    if wd > 0.0:
+        p = round_to(p * F32(1 - lr * wd), dtype)
+    u = round_to(np.asarray(ns_out, dtype=F32), dtype)
+    return round_to(fma32(F32(-lr * scale), u, p), dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -249,12 +249,16 @@ def test_ns5_zero_tile_and_padding(ns_family):
     assert torch.equal(out[1, :37, :100], small[0])
 
 
+@pytest.mark.parametrize("shape", [(2, 256, 512), (2, 128, 128), (2, 128, 256)], ids=["256x512", "128", "128x256"])
 @pytest.mark.parametrize("steps", [0, 1, 2, 5])
-def test_ns5_steps_honoured(steps, ns_family):
-    G = _cpu_randn((2, 256, 512), seed=9).to(DEV)
+def test_ns5_steps_honoured(steps, shape, ns_family):
+    """Every step count, on the stream geometry and on the LDS-resident
+    kernel's (which writes an even step count's result in place)."""
+    G = _cpu_randn(shape, seed=9).to(DEV)
     out = _ns_engine(G, steps=steps)
     ref = torch.from_numpy(O.ns5_staged(G.cpu().numpy(), steps=steps)).to(DEV)
     assert per_tile_rel_fro(out, ref).max() <= 1.5e-2
+    assert torch.equal(out, ns5_torch_staged(G, steps=steps).to(out.dtype))
 
 
 def test_ns5_sub_batch_invariance(ns_family):
