@@ -140,6 +140,8 @@ class TileGroup:
             descs.append(d)
         self.desc = nat.make_desc_table(descs, self.device)
         self._sig = sig
+        # the table holds raw pointers: keep what they point at alive
+        self._bound = (list(grads), list(moms))
         return True
 
     # -- launches ----------------------------------------------------------

@@ -145,7 +145,7 @@ def test_update_tensor_matches_oracle_per_tile():
 
 @pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("cuda_graph", [False, True])
-@pytest.mark.parametrize("tile", [256, (512, 256)])
+@pytest.mark.parametrize("tile", [256, (512, 256), 512])
 def test_fused_untile_apply_matches_unfused(pdt, cuda_graph, tile):
     """The fused untile (WD/LR applied in place, inside the graph) leaves the
     parameters bit-identical to the unfused path (update tensors, then the
