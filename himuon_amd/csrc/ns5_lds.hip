@@ -13,22 +13,28 @@
 //
 // 256 threads = 4 waves. Gram products: the 10 lower 32x32 tiles (ti >= tj
 // of the 4x4 grid of v_mfma_f32_32x32x16_bf16 tiles) are split 3, 3, 2, 2 over
-// the four waves (GramPart), so every SIMD takes part; each strictly lower
-// tile is also written mirrored. A diagonal tile is computed whole and is
+// the four waves (GramPart), so every SIMD takes part. A and B are symmetric
+// and only those 10 tiles are stored (20 KiB): a row fragment of an upper
+// tile (i, k), k > i, is read from the stored tile (k, i) with the
+// contraction along its rows. A diagonal tile is computed whole and is
 // exactly symmetric (element (i, j) and (j, i) sum the same products in the
-// same order). Apply: wave (wm, wn) computes rows 64 wm .. +63 and columns
-// wn np/2 .. + np/2 - 1. Products accumulate in registers; the result
-// replaces its LDS operand after a workgroup barrier. X is read as the MFMA
-// B operand with the contraction along its rows through ds_read_b64_tr_b16.
+// same order), and an off-diagonal tile read transposed holds the values its
+// mirror would, so every operand is the full matrix's, bit for bit. Apply:
+// wave (wm, wn) computes rows 64 wm .. +63 and columns wn np/2 .. + np/2 - 1.
+// Products accumulate in registers; the result replaces its LDS operand after
+// a workgroup barrier. X is read as the MFMA B operand with the contraction
+// along its rows through ds_read_b64_tr_b16.
 // The next tile's X is loaded into registers while the current tile iterates.
 // The k loops are unrolled fully, so the compiler issues later fragment reads
 // ahead of the MFMAs that need them (7 % faster than 2- and 4-fold unrolling).
 //
-// LDS rows hold 16-byte chunks; chunk ch of row r sits at position
+// X rows hold 16-byte chunks; chunk ch of row r sits at position
 // ch ^ s(r), s(r) = 4 (r % 4) + (r / 4) % 4: 16 consecutive rows of one chunk
 // (fragment reads) and 4 consecutive rows of 4 consecutive chunks
-// (transposing reads, mirrored Gram stores) both cover all 16 bank groups.
-// np = 128: 64 KiB per workgroup, two workgroups per CU; np = 256: 96 KiB.
+// (transposing reads) both cover all 16 bank groups. A stored 32x32 tile has
+// 64-byte rows, chunk ch of row r at ch ^ ((r / 4) % 4): 16 consecutive rows
+// of one chunk and 4 consecutive rows of 2 chunks hit distinct bank groups.
+// np = 128: 52 KiB per workgroup, three workgroups per CU; np = 256: 84 KiB.
 #include "ns5_kernels.h"
 
 namespace {
@@ -43,6 +49,14 @@ typedef __attribute__((address_space(3))) u32x4_t lds_u32x4;
 HM_DEV uint32_t lds_pos(int r, int ch, int chunks) {
   const int sw = ((r & 3) << 2) | ((r >> 2) & 3);
   return (uint32_t)(r * chunks + (ch ^ sw)) * 16u;
+}
+
+// Stored lower 32x32 tile (ti >= tj) of a symmetric 128 x 128 matrix:
+// byte offset of 16-byte chunk ch (columns 8 ch ..) of its row r.
+constexpr int TRI_TILE = 32 * 32 * 2;
+constexpr int TRI_BYTES = 10 * TRI_TILE;
+HM_DEV uint32_t tri_pos(int ti, int tj, int r, int ch) {
+  return (uint32_t)((ti * (ti + 1) / 2 + tj) * TRI_TILE + r * 64 + ((ch ^ ((r >> 2) & 3)) << 4));
 }
 
 // Transposing read: 4 bf16 of the 8-byte row segment at `off`, redistributed
@@ -61,6 +75,30 @@ HM_DEV int opaque_lane(int v) {
   return v;
 }
 
+// Row fragment of a symmetric matrix S stored as its lower tiles: lane (l32,
+// hi) receives S[32 R + l32][16 ks + 8 hi .. + 7] (the MFMA operand of row
+// tile R, k-step ks). Column tile k = ks / 2 > R is read from the stored tile
+// (k, R) as the transposing reads of the X operand do.
+template <int R, int KS>
+HM_DEV u32x4_t tri_frag(const lds_u8* S, int l32, int hi, int tr_krow, int tr_col) {
+  constexpr int TK = KS >> 1;
+  if constexpr (TK <= R) {
+    return *reinterpret_cast<lds_cu32x4*>(S + tri_pos(R, TK, l32, 2 * (KS & 1) + hi));
+  } else {
+    const int kr = 16 * (KS & 1) + tr_krow;
+    const u32x2_t l2 = read_tr(S, tri_pos(TK, R, kr, tr_col >> 3) + (tr_col & 7) * 2);
+    const u32x2_t u2 = read_tr(S, tri_pos(TK, R, kr + 4, tr_col >> 3) + (tr_col & 7) * 2);
+    return u32x4_t{l2[0], l2[1], u2[0], u2[1]};
+  }
+}
+
+// Transposing-read lane roles (the X operand of Apply, the upper fragments of
+// A and B): lane (a', b') of each 16-lane group addresses k-row 8 hi + a' (+ 4
+// for the second read) and columns 16 ((lane >> 4) & 1) + 4 b' .. + 3 of a
+// 32-column tile.
+HM_DEV int tr_krow_of(int lane) { return 8 * (lane >> 5) + ((lane & 15) >> 2); }
+HM_DEV int tr_col_of(int lane) { return 16 * ((lane >> 4) & 1) + 4 * (lane & 3); }
+
 // Wave W's share of a Gram product's lower 32x32 tiles: it loads the row tiles
 // ROW[0 .. NR-1] of the operand and computes tiles k < NTL, tile k being
 // (row tile ROW[I[k]], column tile ROW[J[k]]).
@@ -78,51 +116,61 @@ template <> struct GramPart<3> {  // (3,2) (3,3)
   static constexpr int NR = 2, NTL = 2, ROW[3] = {2, 3, 0}, I[3] = {1, 1, 0}, J[3] = {0, 1, 0};
 };
 
+// Fragments of row tile R at k-step KS: from X (SCH chunks per row) or, TRI,
+// from a symmetric matrix stored as its lower tiles.
+template <bool TRI, int SCH, int R, int KS>
+HM_DEV u32x4_t row_frag(const lds_u8* S, int l32, int hi, int tr_krow, int tr_col) {
+  if constexpr (TRI)
+    return tri_frag<R, KS>(S, l32, hi, tr_krow, tr_col);
+  else
+    return *reinterpret_cast<lds_cu32x4*>(S + lds_pos(32 * R + l32, 2 * KS + hi, SCH));
+}
+
+template <int W, bool TRI, int SCH, int KS>
+HM_DEV void gram_step(const lds_u8* S, int l32, int hi, int tr_krow, int tr_col, f32x16_t (&acc)[3]) {
+  using P = GramPart<W>;
+  u32x4_t f[P::NR];
+  f[0] = row_frag<TRI, SCH, P::ROW[0], KS>(S, l32, hi, tr_krow, tr_col);
+  f[1] = row_frag<TRI, SCH, P::ROW[1], KS>(S, l32, hi, tr_krow, tr_col);
+  if constexpr (P::NR > 2) f[2] = row_frag<TRI, SCH, P::ROW[2], KS>(S, l32, hi, tr_krow, tr_col);
+#pragma unroll
+  for (int k = 0; k < P::NTL; ++k) acc[k] = mfma(f[P::J[k]], f[P::I[k]], acc[k]);
+}
+
+template <int W, bool TRI, int SCH, int... KS>
+HM_DEV void gram_steps(const lds_u8* S, int l32, int hi, int tr_krow, int tr_col, f32x16_t (&acc)[3],
+                       std::integer_sequence<int, KS...>) {
+  (gram_step<W, TRI, SCH, KS>(S, l32, hi, tr_krow, tr_col, acc), ...);
+}
+
 // acc[k] = (S S^T) tile k of wave W, S = LDS operand with SCH chunks per row
-// and K = 8 SCH columns. Lane holds element 4 q + e of acc[k] at
+// and K = 8 SCH columns (TRI: a symmetric 128 x 128 matrix stored as its
+// lower tiles). Lane holds element 4 q + e of acc[k] at
 // C[32 ROW[I[k]] + l32][32 ROW[J[k]] + 8 q + 4 hi + e].
-template <int W, int SCH>
+template <int W, bool TRI, int SCH>
 HM_DEV void gram_mma(const lds_u8* S, int lane, f32x16_t (&acc)[3]) {
   using P = GramPart<W>;
   const int ln = opaque_lane(lane), l32 = ln & 31, hi = ln >> 5;
+  const int tr_krow = tr_krow_of(ln), tr_col = tr_col_of(ln);
 #pragma unroll
   for (int k = 0; k < P::NTL; ++k)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[k][e] = 0.f;
-#pragma unroll
-  for (int ks = 0; ks < SCH / 2; ++ks) {
-    u32x4_t f[P::NR];
-#pragma unroll
-    for (int r = 0; r < P::NR; ++r)
-      f[r] = *reinterpret_cast<lds_cu32x4*>(S + lds_pos(32 * P::ROW[r] + l32, 2 * ks + hi, SCH));
-#pragma unroll
-    for (int k = 0; k < P::NTL; ++k) acc[k] = mfma(f[P::J[k]], f[P::I[k]], acc[k]);
-  }
+  gram_steps<W, TRI, SCH>(S, l32, hi, tr_krow, tr_col, acc, std::make_integer_sequence<int, SCH / 2>{});
 }
 
-// Store wave W's bf16 tiles o[k][q] (q: 4 columns each) into the 128 x 128
-// LDS matrix C (ACH chunks per row), and the transpose of every strictly
-// lower tile.
+// Store wave W's bf16 tiles o[k][q] (q: 4 columns each) as lower tiles of
+// the symmetric matrix C.
 template <int W>
 HM_DEV void gram_store(lds_u8* C, int lane, const u32x2_t (&o)[3][4]) {
   using P = GramPart<W>;
-  constexpr int ACH = M / 8;
   const int ln = opaque_lane(lane), l32 = ln & 31, hi = ln >> 5;
 #pragma unroll
   for (int k = 0; k < P::NTL; ++k) {
     const int ti = P::ROW[P::I[k]], tj = P::ROW[P::J[k]];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      *reinterpret_cast<lds_u32x2*>(C + lds_pos(32 * ti + l32, 4 * tj + q, ACH) + hi * 8) = o[k][q];
-      if (ti != tj) {
-        // after the quad transpose, lane (a = l32/4, kk = l32%4) holds
-        // C^T[jt][it .. it + 3], jt = 32 tj + 8 q + 4 hi + kk, it = 32 ti + 4 a
-        const int kk = ln & 3, a = l32 >> 2;
-        const u32x2_t tv = quad_transpose(o[k][q], kk);
-        const int jt = 32 * tj + 8 * q + 4 * hi + kk;
-        *reinterpret_cast<lds_u32x2*>(C + lds_pos(jt, 4 * ti + (a >> 1), ACH) + (a & 1) * 8) = tv;
-      }
-    }
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<lds_u32x2*>(C + tri_pos(ti, tj, l32, q) + hi * 8) = o[k][q];
   }
 }
 
@@ -130,7 +178,7 @@ HM_DEV void gram_store(lds_u8* C, int lane, const u32x2_t (&o)[3][4]) {
 template <int W, int XCH>
 HM_DEV void gram_a(const lds_u8* X, lds_u8* A, int lane) {
   f32x16_t acc[3];
-  gram_mma<W, XCH>(X, lane, acc);
+  gram_mma<W, false, XCH>(X, lane, acc);
   u32x2_t o[3][4];
 #pragma unroll
   for (int k = 0; k < GramPart<W>::NTL; ++k)
@@ -147,14 +195,14 @@ HM_DEV void gram_b(const lds_u8* A, int lane, float cb, float cc, u32x2_t (&o)[3
   using P = GramPart<W>;
   constexpr int ACH = M / 8;
   f32x16_t acc[3];
-  gram_mma<W, ACH>(A, lane, acc);
+  gram_mma<W, true, ACH>(A, lane, acc);
   const int ln = opaque_lane(lane), l32 = ln & 31, hi = ln >> 5;
 #pragma unroll
   for (int k = 0; k < P::NTL; ++k) {
     const int ti = P::ROW[P::I[k]], tj = P::ROW[P::J[k]];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const u32x2_t rv = *reinterpret_cast<lds_cu32x2*>(A + lds_pos(32 * ti + l32, 4 * tj + q, ACH) + hi * 8);
+      const u32x2_t rv = *reinterpret_cast<lds_cu32x2*>(A + tri_pos(ti, tj, l32, q) + hi * 8);
       float y[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) y[e] = fmaf(cb, bf16_to_f32(half16(rv[e >> 1], e & 1)), cc * acc[k][4 * q + e]);
@@ -163,32 +211,59 @@ HM_DEV void gram_b(const lds_u8* A, int lane, float cb, float cc, u32x2_t (&o)[3
   }
 }
 
+// One k-step of Apply for wave row WM: acc[tj][ti] += X^T-column tile tj
+// (transposing reads of X) times B row tile 2 WM + ti.
+template <int TJ, int XCH, int WM, int KS>
+HM_DEV void apply_step(const lds_u8* B, const lds_u8* X, int jb, int l32, int hi, int tr_krow, int tr_col,
+                       f32x16_t (&acc)[TJ][2]) {
+  u32x4_t fb[2], fa[TJ];
+  fb[0] = tri_frag<2 * WM, KS>(B, l32, hi, tr_krow, tr_col);
+  fb[1] = tri_frag<2 * WM + 1, KS>(B, l32, hi, tr_krow, tr_col);
+#pragma unroll
+  for (int tj = 0; tj < TJ; ++tj) {
+    const int c0 = jb + 32 * tj + tr_col;
+    const int kr = 16 * KS + tr_krow;
+    const u32x2_t l2 = read_tr(X, lds_pos(kr, c0 >> 3, XCH) + (c0 & 7) * 2);
+    const u32x2_t u2 = read_tr(X, lds_pos(kr + 4, c0 >> 3, XCH) + (c0 & 7) * 2);
+    fa[tj] = u32x4_t{l2[0], l2[1], u2[0], u2[1]};
+  }
+#pragma unroll
+  for (int tj = 0; tj < TJ; ++tj)
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) acc[tj][ti] = mfma(fa[tj], fb[ti], acc[tj][ti]);
+}
+
+template <int TJ, int XCH, int WM, int... KS>
+HM_DEV void apply_steps(const lds_u8* B, const lds_u8* X, int jb, int lane, f32x16_t (&acc)[TJ][2],
+                        std::integer_sequence<int, KS...>) {
+  const int ln = opaque_lane(lane), l32 = ln & 31, hi = ln >> 5;
+  const int tr_krow = tr_krow_of(ln), tr_col = tr_col_of(ln);
+  (apply_step<TJ, XCH, WM, KS>(B, X, jb, l32, hi, tr_krow, tr_col, acc), ...);
+}
+
 template <int NQ>
-__global__ __launch_bounds__(NT, NQ == 1 ? 2 : 1) void ns5_lds_kernel(const uint16_t* x,
+__global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint16_t* x,
                                                         uint16_t* out,
                                                         const float* __restrict__ inv,
                                                         int64_t ntiles, int steps, float ca,
                                                         float cb, float cc, int round_once) {
   constexpr int N = 128 * NQ;   // NS columns (np)
   constexpr int XCH = N / 8;    // 16-byte chunks per X row
-  constexpr int ACH = M / 8;    // chunks per A row
   __shared__ __attribute__((aligned(16))) uint8_t sx_raw[M * N * 2];
-  __shared__ __attribute__((aligned(16))) uint8_t sa_raw[M * M * 2];
+  __shared__ __attribute__((aligned(16))) uint8_t sa_raw[TRI_BYTES];
   lds_u8* const X = (lds_u8*)sx_raw;
   lds_u8* const A = (lds_u8*)sa_raw;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
-  // Transposing-read lane roles (Apply's X operand): lane (a', b') of each
-  // 16-lane group addresses k-row 8 hi + a' (+ 4 for the second read) and
-  // columns 16 ((lane >> 4) & 1) + 4 b' .. + 3 of a 32-column tile.
-  const int r16 = lane & 15;
-  const int tr_krow = 8 * hi + (r16 >> 2);
-  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (r16 & 3);
 
   constexpr int VPT = M * XCH / NT;  // 16-byte chunks per thread
-  u32x4_t v[VPT];                    // the tile to come, loaded ahead
+  // np = 256 (one workgroup per CU) loads the next tile during this tile's
+  // iterations; np = 128 (three per CU) leaves the load latency to the other
+  // workgroups and keeps the registers.
+  constexpr bool PREFETCH = NQ != 1;
+  u32x4_t v[VPT];
   auto load_tile = [&](int64_t t) {
     const uint16_t* src = x + t * (int64_t)M * N;
 #pragma unroll
@@ -197,10 +272,11 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 2 : 1) void ns5_lds_kernel(const uint
       v[k] = *reinterpret_cast<const u32x4_t*>(src + (int64_t)(idx / XCH) * N + (idx % XCH) * 8);
     }
   };
-  if (blockIdx.x < ntiles) load_tile(blockIdx.x);
+  if (PREFETCH && blockIdx.x < ntiles) load_tile(blockIdx.x);
   for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
     // ---- X0 = bf16(x * inv) into LDS ------------------------------------------
     const float sc = inv[t];
+    if (!PREFETCH) load_tile(t);
     __syncthreads();  // the previous tile's final LDS reads are done
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
@@ -208,7 +284,7 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 2 : 1) void ns5_lds_kernel(const uint
       *reinterpret_cast<lds_u32x4*>(X + lds_pos(idx / XCH, idx % XCH, XCH)) = scale8(v[k], sc);
     }
     // the next tile's loads run under this tile's iterations
-    if (t + gridDim.x < ntiles) load_tile(t + gridDim.x);
+    if (PREFETCH && t + gridDim.x < ntiles) load_tile(t + gridDim.x);
     __syncthreads();
 
     for (int it = 0; it < steps; ++it) {
@@ -251,25 +327,10 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 2 : 1) void ns5_lds_kernel(const uint
           for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < M / 16; ++ks) {
-          u32x4_t fb[2], fa[TJ];
-#pragma unroll
-          for (int t2 = 0; t2 < 2; ++t2)
-            fb[t2] = *reinterpret_cast<lds_cu32x4*>(A + lds_pos(64 * wm + 32 * t2 + l32, 2 * ks + hi, ACH));
-#pragma unroll
-          for (int tj = 0; tj < TJ; ++tj) {
-            const int c0 = jb + 32 * tj + tr_col;
-            const int kr = 16 * ks + tr_krow;
-            const u32x2_t l2 = read_tr(X, lds_pos(kr, c0 >> 3, XCH) + (c0 & 7) * 2);
-            const u32x2_t u2 = read_tr(X, lds_pos(kr + 4, c0 >> 3, XCH) + (c0 & 7) * 2);
-            fa[tj] = u32x4_t{l2[0], l2[1], u2[0], u2[1]};
-          }
-#pragma unroll
-          for (int tj = 0; tj < TJ; ++tj)
-#pragma unroll
-            for (int ti = 0; ti < 2; ++ti) acc[tj][ti] = mfma(fa[tj], fb[ti], acc[tj][ti]);
-        }
+        if (wm == 0)
+          apply_steps<TJ, XCH, 0>(A, X, jb, lane, acc, std::make_integer_sequence<int, M / 16>{});
+        else
+          apply_steps<TJ, XCH, 1>(A, X, jb, lane, acc, std::make_integer_sequence<int, M / 16>{});
         u32x2_t o[2][TJ][4];
 #pragma unroll
         for (int ti = 0; ti < 2; ++ti)
@@ -331,7 +392,7 @@ void ns5_lds_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp
                  float a, float b, float c, bool round_once, hipStream_t s) {
   (void)mp;
   uint16_t* out = (steps & 1) ? y : x;
-  const int64_t wgs = std::min<int64_t>(cnt, (int64_t)(np == 128 ? 2 : 1) * 4 * num_cus());
+  const int64_t wgs = std::min<int64_t>(cnt, (int64_t)(np == 128 ? 3 : 1) * 4 * num_cus());
   if (np == 128)
     hipLaunchKernelGGL(ns5_lds_kernel<1>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
   else
