@@ -590,6 +590,67 @@ def cpu_baseline(layers, shapes, tile, pdtype, budget_s: float = 20.0):
     }
 
 
+def _smi_sample() -> tuple[float, float] | None:
+    """(socket power W, mean gfx clock MHz over the XCDs) from amd-smi."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["amd-smi", "metric", "--power", "--clock", "--json"], capture_output=True,
+                             text=True, timeout=10).stdout
+        d = json.loads(out)
+        g = d["gpu_data"][0] if isinstance(d, dict) else d[0]
+        clks = [v["clk"]["value"] for k, v in g["clock"].items()
+                if k.startswith("gfx_") and isinstance(v.get("clk", {}).get("value"), (int, float))]
+        return float(g["power"]["socket_power"]["value"]), float(np.mean(clks))
+    except Exception:
+        return None
+
+
+def power_probe(opt, seconds: float = 12.0) -> dict:
+    """Board power and shader clock (amd-smi, sampled from a thread every
+    0.3 s) while the NS5 stage runs back to back, and for comparison while a
+    16384^3 bf16 torch.matmul (hipBLASLt) runs: both sit at the board's power
+    limit, which is why the MFMA clock under NS is below the 2.4 GHz behind
+    the published peak."""
+    import threading
+
+    samples, phase, stop = [], ["idle"], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            v = _smi_sample()
+            if v is not None:
+                samples.append((phase[0], *v))
+            time.sleep(0.3)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    time.sleep(2.0)
+    phase[0] = "ns5_stage"
+    t0 = time.time()
+    while time.time() - t0 < seconds:
+        time_ns_stage(opt, 3)
+    phase[0] = "gemm_16384"
+    a = torch.randn(16384, 16384, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn_like(a)
+    t0 = time.time()
+    while time.time() - t0 < seconds * 0.75:
+        for _ in range(8):
+            a @ b
+        torch.cuda.synchronize()
+    phase[0] = "end"
+    stop.set()
+    th.join()
+    out = {}
+    for ph in ("idle", "ns5_stage", "gemm_16384"):
+        v = [(p, c) for q, p, c in samples if q == ph]
+        if v:
+            out[ph] = {"samples": len(v), "power_w_mean": round(float(np.mean([p for p, _ in v])), 1),
+                       "power_w_max": max(p for p, _ in v),
+                       "gfx_clock_mhz_mean": round(float(np.mean([c for _, c in v])), 1)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -606,6 +667,9 @@ def main():
     ap.add_argument("--kernel-only", action="store_true",
                     help="after the warm-up steps, only time the dominant NS kernel (the command the "
                          "rocprofv3 counter passes run) and print its roofline")
+    ap.add_argument("--power", action="store_true",
+                    help="after the warm-up steps, sample board power and shader clock (amd-smi) while "
+                         "the NS5 stage runs, and while a large hipBLASLt GEMM runs, and print them")
     ap.add_argument("--reconfigure", type=int, default=None, metavar="T",
                     help="after the timed steps, reconfigure(tile_size=T) and time the eager "
                          "warm-up steps, the recapture step and the replays of the new regime")
@@ -641,6 +705,9 @@ def main():
     for _ in range(warmup):
         opt.step()
     torch.cuda.synchronize()
+    if args.power:
+        print(json.dumps({"config": args.config, "power": power_probe(opt)}), flush=True)
+        return
     if args.kernel_only:
         dk = time_dominant_kernel(opt, reps=max(3, args.steps))
         print(json.dumps({"config": args.config, "roofline": kernel_roofline(args.config, dk),
