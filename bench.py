@@ -54,12 +54,12 @@ def ns_family(mp: int, np_: int, family: str = "auto") -> str:
     (himuon_ns5_ex dispatch): with family "block128" the 128-blocks
     everywhere; with "stream3" the three streamed 256-block products wherever
     both edges are multiples of 256; with "auto", LDS-resident for mp == 128
-    and np <= 256, the Gram kernel plus the fused GramB/Apply kernel for
+    and np in {128, 256, 512}, the Gram kernel plus the fused GramB/Apply kernel for
     512 x 512 tiles, streamed 256-blocks for other multiples of 256, else
     128-blocks."""
     if family == "block128":
         return "small"
-    if mp == 128 and np_ in (128, 256):
+    if mp == 128 and np_ in (128, 256, 512):
         return "lds"
     if mp % 256 == 0 and np_ % 256 == 0:
         return "fused" if (family == "auto" and mp == 512 and np_ == 512) else "stream"

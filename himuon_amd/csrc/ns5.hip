@@ -320,7 +320,7 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
   uint16_t* wsB = wsA + sb * sq;
   // Family AUTO: tiles whose padded edges are multiples of 256 run the
   // persistent streamed-operand kernels (ns5_stream.hip); tiles with mp == 128
-  // and np <= 256 run the fused LDS-resident kernel (ns5_lds.hip); other tiles
+  // and np in {128, 256, 512} run the fused LDS-resident kernel (ns5_lds.hip); other tiles
   // run the 128-block kernels below, which family BLOCK128 selects for every
   // geometry.
   // 512 x 512 tiles run the first product on the stream kernels and the

@@ -1,5 +1,5 @@
-// Fused Newton-Schulz for NS tiles with mp == 128 (tile edges <= 128): one
-// workgroup keeps a tile's X (128 x np) and its A / B (128 x 128) in LDS
+// Fused Newton-Schulz for NS tiles with mp == 128 and np in {128, 256, 512}:
+// one workgroup keeps a tile's X (128 x np) and its A / B (128 x 128) in LDS
 // through all iterations, so HBM sees one read and one write of the tile.
 // This is the LDS-resident counterpart of the reference's one-kernel NS5 for
 // small tiles (triton_kernels/ns5_smem.py:46-104, dispatched for M*N <= 16384
@@ -7,8 +7,8 @@
 // three-kernel path (XXT.py:55-75, ba_plus_cAA.py:58-85, fused_bmm_add.py:65-88):
 //
 //   X0 = bf16(x * inv)
-//   A  = bf16(X X^T)                    lower 64x64 quadrants, mirrored
-//   B  = bf16(c (A A^T) + b A)          lower 64x64 quadrants, mirrored
+//   A  = bf16(X X^T)                    lower 32x32 tiles only
+//   B  = bf16(c (A A^T) + b A)          lower 32x32 tiles only
 //   X' = bf16(bf16(B X) + a X)
 //
 // 256 threads = 4 waves. Gram products: the 10 lower 32x32 tiles (ti >= tj
@@ -20,10 +20,11 @@
 // exactly symmetric (element (i, j) and (j, i) sum the same products in the
 // same order), and an off-diagonal tile read transposed holds the values its
 // mirror would, so every operand is the full matrix's, bit for bit. Apply:
-// wave (wm, wn) computes rows 64 wm .. +63 and columns wn np/2 .. + np/2 - 1.
-// Products accumulate in registers; the result replaces its LDS operand after
-// a workgroup barrier. X is read as the MFMA B operand with the contraction
-// along its rows through ds_read_b64_tr_b16.
+// wave w owns columns w np/4 .. + np/4 - 1 of all 128 rows (in passes of at
+// most 64 columns) and writes X' over its own columns of X as each pass ends.
+// Products accumulate in registers; B replaces A after a workgroup barrier.
+// X is read as the MFMA B operand with the contraction along its rows through
+// ds_read_b64_tr_b16.
 // The next tile's X is loaded into registers while the current tile iterates.
 // The k loops are unrolled fully, so the compiler issues later fragment reads
 // ahead of the MFMAs that need them (7 % faster than 2- and 4-fold unrolling).
@@ -34,7 +35,8 @@
 // (transposing reads) both cover all 16 bank groups. A stored 32x32 tile has
 // 64-byte rows, chunk ch of row r at ch ^ ((r / 4) % 4): 16 consecutive rows
 // of one chunk and 4 consecutive rows of 2 chunks hit distinct bank groups.
-// np = 128: 52 KiB per workgroup, three workgroups per CU; np = 256: 84 KiB.
+// np = 128: 52 KiB per workgroup, three workgroups per CU; np = 256: 84 KiB,
+// np = 512: 148 KiB, one per CU.
 #include "ns5_kernels.h"
 
 namespace {
@@ -211,14 +213,20 @@ HM_DEV void gram_b(const lds_u8* A, int lane, float cb, float cc, u32x2_t (&o)[3
   }
 }
 
-// One k-step of Apply for wave row WM: acc[tj][ti] += X^T-column tile tj
-// (transposing reads of X) times B row tile 2 WM + ti.
-template <int TJ, int XCH, int WM, int KS>
+// B row-tile fragments R0 .. R0 + RT - 1 at k-step KS.
+template <int R0, int KS, int... R>
+HM_DEV void b_frags(const lds_u8* B, int l32, int hi, int tr_krow, int tr_col, u32x4_t (&fb)[sizeof...(R)],
+                    std::integer_sequence<int, R...>) {
+  ((fb[R] = tri_frag<R0 + R, KS>(B, l32, hi, tr_krow, tr_col)), ...);
+}
+
+// One k-step of Apply: acc[tj][ti] += X^T-column tile tj (transposing reads
+// of X from column jb) times B row tile R0 + ti.
+template <int TJ, int RT, int XCH, int R0, int KS>
 HM_DEV void apply_step(const lds_u8* B, const lds_u8* X, int jb, int l32, int hi, int tr_krow, int tr_col,
-                       f32x16_t (&acc)[TJ][2]) {
-  u32x4_t fb[2], fa[TJ];
-  fb[0] = tri_frag<2 * WM, KS>(B, l32, hi, tr_krow, tr_col);
-  fb[1] = tri_frag<2 * WM + 1, KS>(B, l32, hi, tr_krow, tr_col);
+                       f32x16_t (&acc)[TJ][RT]) {
+  u32x4_t fb[RT], fa[TJ];
+  b_frags<R0, KS>(B, l32, hi, tr_krow, tr_col, fb, std::make_integer_sequence<int, RT>{});
 #pragma unroll
   for (int tj = 0; tj < TJ; ++tj) {
     const int c0 = jb + 32 * tj + tr_col;
@@ -230,15 +238,15 @@ HM_DEV void apply_step(const lds_u8* B, const lds_u8* X, int jb, int l32, int hi
 #pragma unroll
   for (int tj = 0; tj < TJ; ++tj)
 #pragma unroll
-    for (int ti = 0; ti < 2; ++ti) acc[tj][ti] = mfma(fa[tj], fb[ti], acc[tj][ti]);
+    for (int ti = 0; ti < RT; ++ti) acc[tj][ti] = mfma(fa[tj], fb[ti], acc[tj][ti]);
 }
 
-template <int TJ, int XCH, int WM, int... KS>
-HM_DEV void apply_steps(const lds_u8* B, const lds_u8* X, int jb, int lane, f32x16_t (&acc)[TJ][2],
+template <int TJ, int RT, int XCH, int R0, int... KS>
+HM_DEV void apply_steps(const lds_u8* B, const lds_u8* X, int jb, int lane, f32x16_t (&acc)[TJ][RT],
                         std::integer_sequence<int, KS...>) {
   const int ln = opaque_lane(lane), l32 = ln & 31, hi = ln >> 5;
   const int tr_krow = tr_krow_of(ln), tr_col = tr_col_of(ln);
-  (apply_step<TJ, XCH, WM, KS>(B, X, jb, l32, hi, tr_krow, tr_col, acc), ...);
+  (apply_step<TJ, RT, XCH, R0, KS>(B, X, jb, l32, hi, tr_krow, tr_col, acc), ...);
 }
 
 template <int NQ>
@@ -256,13 +264,13 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
-  const int wm = wave >> 1, wn = wave & 1;
 
   constexpr int VPT = M * XCH / NT;  // 16-byte chunks per thread
   // np = 256 (one workgroup per CU) loads the next tile during this tile's
   // iterations; np = 128 (three per CU) leaves the load latency to the other
-  // workgroups and keeps the registers.
-  constexpr bool PREFETCH = NQ != 1;
+  // workgroups and keeps the registers; np = 512 has no registers to spare
+  // for a whole tile.
+  constexpr bool PREFETCH = NQ == 2;
   u32x4_t v[VPT];
   auto load_tile = [&](int64_t t) {
     const uint16_t* src = x + t * (int64_t)M * N;
@@ -317,50 +325,53 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint
       __syncthreads();
 
       // ---- X' = bf16(bf16(B X) + a X), in place of X ------------------------------
+      // Wave w owns columns w np/4 .. + np/4 - 1 over all 128 rows, in passes of
+      // at most 64 columns. It reads only its own columns of X, so it
+      // overwrites them as each pass ends, without waiting for the other waves.
       {
-        constexpr int TJ = 2 * NQ;  // 32-column tiles per wave
-        const int jb = wn * (N / 2);
-        f32x16_t acc[TJ][2];
+        constexpr int WCOL = N / 4;                 // columns per wave
+        constexpr int PT = WCOL >= 64 ? 2 : 1;      // 32-column tiles per pass
+#pragma unroll 1
+        for (int pass = 0; pass < WCOL / (32 * PT); ++pass) {
+          const int jb = WCOL * wave + 32 * PT * pass;
+          f32x16_t acc[PT][4];
 #pragma unroll
-        for (int a = 0; a < TJ; ++a)
+          for (int a = 0; a < PT; ++a)
 #pragma unroll
-          for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < 4; ++b)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
-        if (wm == 0)
-          apply_steps<TJ, XCH, 0>(A, X, jb, lane, acc, std::make_integer_sequence<int, M / 16>{});
-        else
-          apply_steps<TJ, XCH, 1>(A, X, jb, lane, acc, std::make_integer_sequence<int, M / 16>{});
-        u32x2_t o[2][TJ][4];
+              for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+          apply_steps<PT, 4, XCH, 0>(A, X, jb, lane, acc, std::make_integer_sequence<int, M / 16>{});
+          u32x2_t o[4][PT][4];
 #pragma unroll
-        for (int ti = 0; ti < 2; ++ti)
+          for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
-          for (int tj = 0; tj < TJ; ++tj)
+            for (int tj = 0; tj < PT; ++tj)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int i = 64 * wm + 32 * ti + l32;
-              const int ch = (jb >> 3) + 4 * tj + q;
-              const u32x2_t rv = *reinterpret_cast<lds_cu32x2*>(X + lds_pos(i, ch, XCH) + hi * 8);
-              float y[4];
+              for (int q = 0; q < 4; ++q) {
+                const int i = 32 * ti + l32;
+                const int ch = (jb >> 3) + 4 * tj + q;
+                const u32x2_t rv = *reinterpret_cast<lds_cu32x2*>(X + lds_pos(i, ch, XCH) + hi * 8);
+                float y[4];
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const float v = acc[tj][ti][4 * q + e];
-                const float bx = round_once ? v : bf16_to_f32(pk_bf16(v, 0.f) & 0xffffu);
-                y[e] = fmaf(ca, bf16_to_f32(half16(rv[e >> 1], e & 1)), bx);
+                for (int e = 0; e < 4; ++e) {
+                  const float v = acc[tj][ti][4 * q + e];
+                  const float bx = round_once ? v : bf16_to_f32(pk_bf16(v, 0.f) & 0xffffu);
+                  y[e] = fmaf(ca, bf16_to_f32(half16(rv[e >> 1], e & 1)), bx);
+                }
+                o[ti][tj][q] = u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
               }
-              o[ti][tj][q] = u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
-            }
-        __syncthreads();  // every read of X is done
 #pragma unroll
-        for (int ti = 0; ti < 2; ++ti)
+          for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
-          for (int tj = 0; tj < TJ; ++tj)
+            for (int tj = 0; tj < PT; ++tj)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int i = 64 * wm + 32 * ti + l32;
-              const int ch = (jb >> 3) + 4 * tj + q;
-              *reinterpret_cast<lds_u32x2*>(X + lds_pos(i, ch, XCH) + hi * 8) = o[ti][tj][q];
-            }
+              for (int q = 0; q < 4; ++q) {
+                const int i = 32 * ti + l32;
+                const int ch = (jb >> 3) + 4 * tj + q;
+                *reinterpret_cast<lds_u32x2*>(X + lds_pos(i, ch, XCH) + hi * 8) = o[ti][tj][q];
+              }
+        }
       }
       __syncthreads();
     }
@@ -386,7 +397,7 @@ int num_cus() {
 
 }  // namespace
 
-bool ns5_lds_supported(int mp, int np) { return mp == M && (np == 128 || np == 256); }
+bool ns5_lds_supported(int mp, int np) { return mp == M && (np == 128 || np == 256 || np == 512); }
 
 void ns5_lds_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
                  float a, float b, float c, bool round_once, hipStream_t s) {
@@ -395,6 +406,8 @@ void ns5_lds_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp
   const int64_t wgs = std::min<int64_t>(cnt, (int64_t)(np == 128 ? 3 : 1) * 4 * num_cus());
   if (np == 128)
     hipLaunchKernelGGL(ns5_lds_kernel<1>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
-  else
+  else if (np == 256)
     hipLaunchKernelGGL(ns5_lds_kernel<2>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
+  else
+    hipLaunchKernelGGL(ns5_lds_kernel<4>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
 }

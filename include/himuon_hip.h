@@ -137,7 +137,7 @@ size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np);
  * in x when `steps` is even and in y when it is odd (the other buffer's
  * contents are unspecified afterwards; x and y must not alias). X0 is formed
  * by the first iteration's kernels as they read x, not by a separate pass.
- * Tiles with mp == 128 and np <= 256 run all iterations
+ * Tiles with mp == 128 and np in {128, 256, 512} run all iterations
  * of a tile inside one workgroup's LDS; 512 x 512 tiles run the first
  * product on a persistent 256x256-block kernel and the other two fused
  * (himuon_ba_bmm_add's kernel); other tiles whose mp and np are multiples of

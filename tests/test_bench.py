@@ -15,9 +15,11 @@ import bench  # noqa: E402
 
 
 def test_ns_family_follows_the_library_dispatch():
-    # LDS-resident kernel: mp == 128 and np <= 256
+    # LDS-resident kernel: mp == 128 and np in {128, 256, 512}
     assert bench.ns_family(128, 128) == "lds"
     assert bench.ns_family(128, 256) == "lds"
+    assert bench.ns_family(128, 512) == "lds"
+    assert bench.ns_family(128, 384) == "small" and bench.ns_family(128, 1024) == "small"
     # 512 x 512: Gram kernel + fused GramB/Apply; the three products with "stream3"
     assert bench.ns_family(512, 512) == "fused"
     assert bench.ns_family(512, 512, "stream3") == "stream"

@@ -164,6 +164,7 @@ NS_SHAPES = [
     ("square_128", (4, 128, 128)),
     ("square_64", (8, 64, 64)),
     ("wide_64x256", (4, 64, 256)),
+    ("wide_128x512", (4, 128, 512)),
     ("tall_128x64", (4, 128, 64)),
     ("big_512", (4, 512, 512)),
     ("2d_square_512", (512, 512)),
@@ -249,7 +250,8 @@ def test_ns5_zero_tile_and_padding(ns_family):
     assert torch.equal(out[1, :37, :100], small[0])
 
 
-@pytest.mark.parametrize("shape", [(2, 256, 512), (2, 128, 128), (2, 128, 256)], ids=["256x512", "128", "128x256"])
+@pytest.mark.parametrize("shape", [(2, 256, 512), (2, 128, 128), (2, 128, 256), (2, 128, 512)],
+                         ids=["256x512", "128", "128x256", "128x512"])
 @pytest.mark.parametrize("steps", [0, 1, 2, 5])
 def test_ns5_steps_honoured(steps, shape, ns_family):
     """Every step count, on the stream geometry and on the LDS-resident
@@ -279,6 +281,7 @@ STALE_SHAPES = [
     # (label, n, M, N): one per kernel family / geometry class
     ("lds_128", 3, 128, 128),
     ("lds_100x200", 3, 100, 200),
+    ("lds_100x400", 3, 100, 400),
     ("blk_100x300", 3, 100, 300),
     ("blk_tall_300x100", 3, 300, 100),
     ("blk_300x300", 2, 300, 300),
