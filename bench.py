@@ -82,7 +82,8 @@ KERNEL_TRAFFIC = {
 }
 KERNEL_SOURCES = {
     "ns_ba_kernel": ["ns5_ba.hip", "ns5_kernels.h", "common.h"],
-    "ns5_lds_kernel": ["ns5_lds.hip", "ns5_kernels.h", "common.h"],
+    "ns5_lds_kernel": ["ns5_lds.hip", "ns5_kernels.h", "common.h", "elem_ops.h"],
+    "lds_step_kernel": ["ns5_lds.hip", "ns5_kernels.h", "common.h", "elem_ops.h"],
     "ns_st_kernel": ["ns5_stream.hip", "ns5_kernels.h", "common.h"],
 }
 
@@ -168,6 +169,24 @@ def time_ns_stage(opt, reps: int) -> float:
     return sum(e0.elapsed_time(e1) for e0, e1 in evs) / reps
 
 
+def time_lds_step_stage(opt, reps: int) -> float | None:
+    """Average ms of the step's LDS-resident launches (himuon_lds_step, one
+    per chunk: momentum to WD/LR) over every group that runs them; None when
+    no group does."""
+    groups = [g for g in opt._groups if opt._fuse_lds_step and g["tiles"].lds_step_ok()]
+    if not groups:
+        return None
+
+    def run():
+        for g in groups:
+            ofs = 0
+            for c in g["chunks"]:
+                g["tiles"].lds_step(ofs, c, g["steps"], opt._lrwd)
+                ofs += c
+
+    return _event_loop(run, reps)
+
+
 def _event_loop(fn, reps: int, prep=None) -> float:
     """Average ms of fn() over reps runs, HIP events around each run on the
     current stream (the stream the library launches on); prep() runs
@@ -205,6 +224,16 @@ def time_dominant_kernel(opt, reps: int) -> dict:
     grp = g["tiles"]
     fam = ns_family(grp.mp, grp.np)
     n = min(g["sub_batch"], grp.n_tiles)
+    if opt._fuse_lds_step and grp.lds_step_ok():
+        # the whole step of n tiles in one launch (himuon_lds_step): the
+        # momentum buffers and parameters of those tiles are read and written
+        # once each, the grads read once
+        ms = _event_loop(lambda: grp.lds_step(0, n, g["steps"], opt._lrwd), reps)
+        gb = torch.empty(0, dtype=grp.dtype).element_size()
+        pb = torch.empty(0, dtype=grp.upd_dtype).element_size()
+        return {"kernel": "lds_step_kernel", "family": "lds_step", "launch_tiles": n, "launch_ms": ms,
+                "flops_per_launch": float(ns_flops(grp.m, grp.n)) * n,
+                "bytes_per_launch": float(_tile_elements(grp, n)) * (3 * gb + 2 * pb)}
     m, nn = grp.mp, grp.np
     x, y, inv = grp.tiles[:n], grp.alt[:n], grp.inv[:n]
     if fam == "fused":
@@ -225,12 +254,48 @@ def time_dominant_kernel(opt, reps: int) -> dict:
             "flops_per_launch": float(ns_flops(grp.m, grp.n)) * n}
 
 
+def _tile_elements(grp, n: int) -> int:
+    """Parameter elements covered by the group's first n bucket tiles."""
+    total = 0
+    for p, t0, cnt in zip(grp.params, grp.tile0, grp.tile_counts):
+        h, w = p.shape
+        C = -(-w // grp.tile_w)
+        for lt in range(max(0, min(cnt, n - t0))):
+            r, c = divmod(lt, C)
+            total += min(grp.tile_h, h - r * grp.tile_h) * min(grp.tile_w, w - c * grp.tile_w)
+    return total
+
+
 def kernel_roofline(config: str, dk: dict) -> dict:
     tflops = dk["flops_per_launch"] / (dk["launch_ms"] * 1e-3) / 1e12
     entry = KERNEL_TRAFFIC.get((config, dk["kernel"]))
     traffic = None
     if entry is not None and dk["kernel"] in KERNEL_SOURCES and entry[1] == sources_digest(dk["kernel"]):
         traffic = entry[0]
+    if "bytes_per_launch" in dk:
+        # both bounds apply; the roofline's binding one is the lower ceiling:
+        # HBM when the algorithmic intensity is below the ridge point
+        gbs = dk["bytes_per_launch"] / (dk["launch_ms"] * 1e-3) / 1e9
+        hbm = dk["flops_per_launch"] / dk["bytes_per_launch"] < PEAK_BF16_TFLOPS * 1e3 / PEAK_HBM_GBS
+        out = {
+            "kernel": f"{dk['kernel']} ({dk['launch_tiles']} tiles per launch)",
+            "bound": "hbm" if hbm else "mfma",
+            "achieved": round(gbs, 1) if hbm else round(tflops, 1),
+            "peak": PEAK_HBM_GBS if hbm else PEAK_BF16_TFLOPS,
+            "unit": "GB/s" if hbm else "TFLOP/s",
+            "frac": round(gbs / PEAK_HBM_GBS if hbm else tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic,
+            "launch_ms": round(dk["launch_ms"], 4),
+            "flops_per_launch": dk["flops_per_launch"],
+            "bytes_per_launch": dk["bytes_per_launch"],
+            "tflops": round(tflops, 1),
+            "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+            "hbm_gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+        }
+        if traffic:
+            out["traffic_gbs"] = round(traffic / (dk["launch_ms"] * 1e-3) / 1e9, 1)
+        return out
     out = {
         "kernel": f"{dk['kernel']} ({dk['launch_tiles']} tiles per launch)",
         "bound": "mfma",
@@ -739,6 +804,7 @@ def main():
     ns_ms = time_ns_stage(opt, reps=max(3, args.steps // 2))
     dk = time_dominant_kernel(opt, reps=max(3, args.steps // 2))
     gather_ms, untile_ms = time_io_stage(opt, reps=max(3, args.steps // 2))
+    lds_step_ms = time_lds_step_stage(opt, reps=max(3, args.steps // 2))
     apply_ms = time_apply(opt, reps=max(3, args.steps // 2))
     flops = algorithmic_flops(opt)
     n_tiles = sum(g["tiles"].n_tiles for g in opt._groups)
@@ -784,10 +850,15 @@ def main():
         "untile_ms": round(untile_ms, 3),
         "untile_gbs": round(((2 + 2 * pb) if fused else (2 + ub)) * n_el / (untile_ms * 1e-3) / 1e9, 1),
         "untile_applies_wd_lr": fused,
+        # 128 x 128-tile buckets run the whole step as one LDS-resident launch
+        # per chunk; ns5/gather/untile above then time the launches it replaces
+        "lds_step_ms": None if lds_step_ms is None else round(lds_step_ms, 3),
         "apply_ms": round(apply_ms, 3),
         "apply_gbs": None if fused else round((2 * pb + ub) * n_el / (apply_ms * 1e-3) / 1e9, 1),
         "update_dtype": None if fused else str(opt._groups[0]["tiles"].upd_dtype).replace("torch.", ""),
-        "ns5_stage_kernels": "; ".join(NS_KERNELS[f] for f in fams),
+        "ns5_stage_kernels": ("step: lds_step_kernel (momentum, gather, normaliser, NS5 and untile with "
+                              "WD/LR of 128x128 tiles in one launch per chunk)" if lds_step_ms is not None
+                              else "; ".join(NS_KERNELS[f] for f in fams)),
         # the dominant kernel, one launch on one sub-batch (HIP events)
         "roofline": kernel_roofline(args.config, dk),
     }

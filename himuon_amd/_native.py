@@ -129,6 +129,8 @@ _SIGNATURES = {
     "himuon_bmm_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_int, c_void_p]),
     "himuon_ba_bmm_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_float, c_float,
                                   c_int, c_void_p]),
+    "himuon_lds_step": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int, c_int, c_int, c_int, c_int, c_float,
+                                c_float, c_float, c_float, c_int, c_void_p, c_void_p]),
     "himuon_ns5_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_float, c_float,
                                    c_float, c_int, c_void_p]),
     "himuon_untile": (
@@ -342,6 +344,28 @@ def ba_bmm_add(a, x, out, batch, alpha, beta, gamma, round_once=False):
     chip (512 x 512 tiles; bf16(B X + gamma X) with round_once)."""
     _check(load().himuon_ba_bmm_add(a.data_ptr(), x.data_ptr(), out.data_ptr(), batch, 512, 512, alpha, beta, gamma,
                                     NS_ROUND_ONCE if round_once else 0, _stream()), "himuon_ba_bmm_add")
+
+
+def lds_step_supported(tile_h: int, tile_w: int, dtype, param_dtype) -> bool:
+    """Buckets himuon_lds_step takes: 128 x 128 NS tiles without transpose,
+    fp32/bf16 grads and parameters, unless the 128-block family is forced."""
+    return (0 < tile_h <= tile_w <= 128 and dtype in (torch.float32, torch.bfloat16)
+            and param_dtype in (torch.float32, torch.bfloat16) and ns_family_override != "block128")
+
+
+def lds_step(desc_table, n_params, tile_begin, n_tiles, tile_h, tile_w, dtype, param_dtype, steps, scale_alpha,
+             round_once=False, coeffs=(NS_A, NS_B, NS_C), eps=NS_EPS):
+    """Momentum, gather, normaliser, NS5 and the untile with WD/LR for bucket
+    tiles tile_begin .. + n_tiles - 1 in one launch (128 x 128 NS tiles)."""
+    a, b, c = coeffs
+    _check(
+        load().himuon_lds_step(
+            desc_table.data_ptr(), n_params, tile_begin, n_tiles, tile_h, tile_w, dtype_code(dtype),
+            dtype_code(param_dtype), steps, a, b, c, eps, NS_ROUND_ONCE if round_once else 0,
+            scale_alpha.data_ptr(), _stream(),
+        ),
+        "himuon_lds_step",
+    )
 
 
 def untile(desc_table, n_params, n_tiles, tile_h, tile_w, mp, np_, dtype, tiles):

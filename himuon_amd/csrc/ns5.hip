@@ -407,6 +407,19 @@ void* scratch_address(int* err) {
 }
 }  // namespace
 
+extern "C" int himuon_lds_step(const HimuonParamDesc* params_dev, int n_params, int64_t tile_begin,
+                               int64_t n_tiles, int tile_h, int tile_w, int dtype, int param_dtype, int steps,
+                               float a, float b, float c, float eps, int flags, const float* scale_alpha_dev,
+                               void* stream) {
+  if (!params_dev || n_params <= 0 || tile_begin < 0 || n_tiles < 0 || steps < 0 || !scale_alpha_dev ||
+      (flags & ~HIMUON_NS_ROUND_ONCE) || !lds_step_supported(tile_h, tile_w, dtype, param_dtype))
+    return HIMUON_EINVAL;
+  if (n_tiles == 0) return 0;
+  lds_step_run(params_dev, n_params, tile_begin, n_tiles, tile_h, tile_w, dtype, param_dtype, steps, a, b, c,
+               eps, (flags & HIMUON_NS_ROUND_ONCE) != 0, scale_alpha_dev, static_cast<hipStream_t>(stream));
+  return (int)hipGetLastError();
+}
+
 extern "C" int himuon_ns5_noalloc(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp,
                                   int np, int steps, float a, float b, float c, int flags, void* stream) {
   if (!x || !y || x == y || !inv || n_tiles < 0 || steps < 0 || mp <= 0 || np <= 0 || mp > np ||

@@ -170,6 +170,14 @@ void ns_stream_product(int mode, const uint16_t* P, int64_t p_bs, int ldp, const
 // Fused LDS-resident path (ns5_lds.hip): mp == 128, np = 128 or 256. Runs
 // `steps` >= 1 iterations of `cnt` tiles in one launch; reads X from x and
 // leaves the result in x (even `steps`) or y (odd), as the other paths do.
+// The whole step of a bucket of NS tiles with tile_h <= tile_w <= 128 in one
+// launch (ns5_lds.hip): momentum + gather + normaliser + NS5 + untile with
+// WD/LR, on bucket tiles tile_begin .. tile_begin + cnt - 1; grad/momentum
+// dtype `dtype`, parameter dtype `param_dtype` (fp32 or bf16 each).
+bool lds_step_supported(int tile_h, int tile_w, int dtype, int param_dtype);
+void lds_step_run(const HimuonParamDesc* params, int n_params, int64_t tile_begin, int64_t cnt, int tile_h,
+                  int tile_w, int dtype, int param_dtype, int steps, float a, float b, float c, float eps,
+                  bool round_once, const float* sa, hipStream_t s);
 bool ns5_lds_supported(int mp, int np);
 void ns5_lds_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
                  float a, float b, float c, bool round_once, hipStream_t s);

@@ -37,6 +37,7 @@
 // of one chunk and 4 consecutive rows of 2 chunks hit distinct bank groups.
 // np = 128: 52 KiB per workgroup, three workgroups per CU; np = 256: 84 KiB,
 // np = 512: 148 KiB, one per CU.
+#include "elem_ops.h"
 #include "ns5_kernels.h"
 
 namespace {
@@ -249,6 +250,98 @@ HM_DEV void apply_steps(const lds_u8* B, const lds_u8* X, int jb, int lane, f32x
   (apply_step<TJ, RT, XCH, R0, KS>(B, X, jb, l32, hi, tr_krow, tr_col, acc), ...);
 }
 
+// `steps` NS iterations on the tile X0 in LDS (X, 128 x 128 NQ), A/B in the
+// lower-tile buffer A; X' replaces X. Every thread of the workgroup calls it;
+// it ends with a workgroup barrier.
+template <int NQ>
+HM_DEV void ns_iterations(lds_u8* X, lds_u8* A, int lane, int steps, float ca, float cb, float cc,
+                          int round_once) {
+  constexpr int N = 128 * NQ;
+  constexpr int XCH = N / 8;
+  const int wave = threadIdx.x >> 6;
+  for (int it = 0; it < steps; ++it) {
+    // ---- A = bf16(X X^T) ------------------------------------------------------
+    switch (wave) {
+      case 0: gram_a<0, XCH>(X, A, lane); break;
+      case 1: gram_a<1, XCH>(X, A, lane); break;
+      case 2: gram_a<2, XCH>(X, A, lane); break;
+      default: gram_a<3, XCH>(X, A, lane); break;
+    }
+    __syncthreads();
+
+    // ---- B = bf16(c (A A^T) + b A), in place of A --------------------------------
+    {
+      u32x2_t o[3][4];
+      switch (wave) {
+        case 0: gram_b<0>(A, lane, cb, cc, o); break;
+        case 1: gram_b<1>(A, lane, cb, cc, o); break;
+        case 2: gram_b<2>(A, lane, cb, cc, o); break;
+        default: gram_b<3>(A, lane, cb, cc, o); break;
+      }
+      __syncthreads();  // every read of A (products and the b A term) is done
+      switch (wave) {
+        case 0: gram_store<0>(A, lane, o); break;
+        case 1: gram_store<1>(A, lane, o); break;
+        case 2: gram_store<2>(A, lane, o); break;
+        default: gram_store<3>(A, lane, o); break;
+      }
+    }
+    __syncthreads();
+
+    // ---- X' = bf16(bf16(B X) + a X), in place of X ------------------------------
+    // Wave w owns columns w np/4 .. + np/4 - 1 over all 128 rows, in passes of
+    // at most 64 columns. It reads only its own columns of X, so it
+    // overwrites them as each pass ends, without waiting for the other waves.
+    {
+      constexpr int WCOL = N / 4;                 // columns per wave
+      constexpr int PT = WCOL >= 64 ? 2 : 1;      // 32-column tiles per pass
+#pragma unroll 1
+      for (int pass = 0; pass < WCOL / (32 * PT); ++pass) {
+        const int jb = WCOL * wave + 32 * PT * pass;
+        f32x16_t acc[PT][4];
+#pragma unroll
+        for (int a = 0; a < PT; ++a)
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+        apply_steps<PT, 4, XCH, 0>(A, X, jb, lane, acc, std::make_integer_sequence<int, M / 16>{});
+        const int ln = opaque_lane(lane), l32 = ln & 31, hi = ln >> 5;
+        u32x2_t o[4][PT][4];
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+          for (int tj = 0; tj < PT; ++tj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int i = 32 * ti + l32;
+              const int ch = (jb >> 3) + 4 * tj + q;
+              const u32x2_t rv = *reinterpret_cast<lds_cu32x2*>(X + lds_pos(i, ch, XCH) + hi * 8);
+              float y[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float v = acc[tj][ti][4 * q + e];
+                const float bx = round_once ? v : bf16_to_f32(pk_bf16(v, 0.f) & 0xffffu);
+                y[e] = fmaf(ca, bf16_to_f32(half16(rv[e >> 1], e & 1)), bx);
+              }
+              o[ti][tj][q] = u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
+            }
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+          for (int tj = 0; tj < PT; ++tj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int i = 32 * ti + l32;
+              const int ch = (jb >> 3) + 4 * tj + q;
+              *reinterpret_cast<lds_u32x2*>(X + lds_pos(i, ch, XCH) + hi * 8) = o[ti][tj][q];
+            }
+      }
+    }
+    __syncthreads();
+  }
+}
+
 template <int NQ>
 __global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint16_t* x,
                                                         uint16_t* out,
@@ -295,86 +388,7 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint
     if (PREFETCH && t + gridDim.x < ntiles) load_tile(t + gridDim.x);
     __syncthreads();
 
-    for (int it = 0; it < steps; ++it) {
-      // ---- A = bf16(X X^T) ------------------------------------------------------
-      switch (wave) {
-        case 0: gram_a<0, XCH>(X, A, lane); break;
-        case 1: gram_a<1, XCH>(X, A, lane); break;
-        case 2: gram_a<2, XCH>(X, A, lane); break;
-        default: gram_a<3, XCH>(X, A, lane); break;
-      }
-      __syncthreads();
-
-      // ---- B = bf16(c (A A^T) + b A), in place of A --------------------------------
-      {
-        u32x2_t o[3][4];
-        switch (wave) {
-          case 0: gram_b<0>(A, lane, cb, cc, o); break;
-          case 1: gram_b<1>(A, lane, cb, cc, o); break;
-          case 2: gram_b<2>(A, lane, cb, cc, o); break;
-          default: gram_b<3>(A, lane, cb, cc, o); break;
-        }
-        __syncthreads();  // every read of A (products and the b A term) is done
-        switch (wave) {
-          case 0: gram_store<0>(A, lane, o); break;
-          case 1: gram_store<1>(A, lane, o); break;
-          case 2: gram_store<2>(A, lane, o); break;
-          default: gram_store<3>(A, lane, o); break;
-        }
-      }
-      __syncthreads();
-
-      // ---- X' = bf16(bf16(B X) + a X), in place of X ------------------------------
-      // Wave w owns columns w np/4 .. + np/4 - 1 over all 128 rows, in passes of
-      // at most 64 columns. It reads only its own columns of X, so it
-      // overwrites them as each pass ends, without waiting for the other waves.
-      {
-        constexpr int WCOL = N / 4;                 // columns per wave
-        constexpr int PT = WCOL >= 64 ? 2 : 1;      // 32-column tiles per pass
-#pragma unroll 1
-        for (int pass = 0; pass < WCOL / (32 * PT); ++pass) {
-          const int jb = WCOL * wave + 32 * PT * pass;
-          f32x16_t acc[PT][4];
-#pragma unroll
-          for (int a = 0; a < PT; ++a)
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-#pragma unroll
-              for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
-          apply_steps<PT, 4, XCH, 0>(A, X, jb, lane, acc, std::make_integer_sequence<int, M / 16>{});
-          u32x2_t o[4][PT][4];
-#pragma unroll
-          for (int ti = 0; ti < 4; ++ti)
-#pragma unroll
-            for (int tj = 0; tj < PT; ++tj)
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const int i = 32 * ti + l32;
-                const int ch = (jb >> 3) + 4 * tj + q;
-                const u32x2_t rv = *reinterpret_cast<lds_cu32x2*>(X + lds_pos(i, ch, XCH) + hi * 8);
-                float y[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  const float v = acc[tj][ti][4 * q + e];
-                  const float bx = round_once ? v : bf16_to_f32(pk_bf16(v, 0.f) & 0xffffu);
-                  y[e] = fmaf(ca, bf16_to_f32(half16(rv[e >> 1], e & 1)), bx);
-                }
-                o[ti][tj][q] = u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
-              }
-#pragma unroll
-          for (int ti = 0; ti < 4; ++ti)
-#pragma unroll
-            for (int tj = 0; tj < PT; ++tj)
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const int i = 32 * ti + l32;
-                const int ch = (jb >> 3) + 4 * tj + q;
-                *reinterpret_cast<lds_u32x2*>(X + lds_pos(i, ch, XCH) + hi * 8) = o[ti][tj][q];
-              }
-        }
-      }
-      __syncthreads();
-    }
+    ns_iterations<NQ>(X, A, lane, steps, ca, cb, cc, round_once);
 
     // ---- result -> global ----------------------------------------------------------
     uint16_t* dst = out + t * (int64_t)M * N;
@@ -383,6 +397,156 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint
       const int idx = k * NT + tid;
       *reinterpret_cast<u32x4_t*>(dst + (int64_t)(idx / XCH) * N + (idx % XCH) * 8) =
           *reinterpret_cast<lds_cu32x4*>(X + lds_pos(idx / XCH, idx % XCH, XCH));
+    }
+  }
+}
+
+// The whole optimizer step of a bucket of 128 x 128 NS tiles in one launch
+// (tile_h <= tile_w <= 128, so no transpose): per tile, the momentum update
+// and gather (the gather kernel's arithmetic), the normaliser, the NS
+// iterations and the untile with WD/LR (the fused untile's arithmetic), with
+// the tile held in LDS from the momentum to the parameter update. HBM sees the
+// grad, the momentum buffer (read and written) and the parameter (read and
+// written) once each; no NS tile buffer exists.
+//
+// Bit-identical to gather -> tile_scale -> NS5 -> untile_apply: every element
+// is computed by the same per-element code, and the tile's sum of squares is
+// accumulated in the gather kernel's order (256 threads; thread t sums the
+// 8-element vectors t, t + 256, ..., t + 1792 of the 128 x 128 tile, each in
+// element order; then the same wave and block reductions, and the same
+// 1 / (sqrt(s) + eps)).
+template <int DT, int PDT>
+__global__ __launch_bounds__(NT, 3) void lds_step_kernel(const HimuonParamDesc* __restrict__ params, int n_params,
+                                                         int64_t tile_begin, int64_t ntiles, int tile_h,
+                                                         int tile_w, int steps, float ca, float cb, float cc,
+                                                         float eps, int round_once,
+                                                         const float* __restrict__ sa) {
+  constexpr int N = 128, XCH = N / 8, VPR = N / 8;  // 16 vectors of 8 per NS row
+  constexpr int VPT = M * VPR / NT;                  // vectors per thread (8)
+  constexpr int BATCH = 2;                           // vectors loaded before any is used
+  __shared__ __attribute__((aligned(16))) uint8_t sx_raw[M * N * 2];
+  __shared__ __attribute__((aligned(16))) uint8_t sa_raw[TRI_BYTES];
+  __shared__ float red[NT / 64];
+  __shared__ float s_inv;
+  lds_u8* const X = (lds_u8*)sx_raw;
+  lds_u8* const A = (lds_u8*)sa_raw;
+  const int tid = threadIdx.x, lane = tid & 63;
+
+  for (int64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
+    const int64_t t = tile_begin + tt;
+    __syncthreads();  // the previous tile's untile reads of X are done
+    const HimuonParamDesc& P = params[find_param(params, n_params, t)];
+    const int64_t lt = t - P.tile0;
+    const int r = (int)(lt / P.C), c = (int)(lt % P.C);
+    const bool has_mom = P.momentum != nullptr;
+    const float mu = P.mu;
+    const bool nesterov = P.nesterov != 0;
+
+    // ---- momentum + bf16(e) + sum of squares (the gather) ----------------------
+    // (thread-dependent addresses from an opaque copy of the thread index in
+    // each phase: hoisted out of the tile loop they would not fit beside the
+    // NS iterations' registers)
+    const int tg = opaque_lane(tid);
+    float ssq = 0.f;
+    // bf16(e) goes to LDS as it is formed; the normaliser is applied in
+    // place once the tile's sum is known (each thread rescales its own
+    // vectors)
+#pragma unroll 1
+    for (int b0 = 0; b0 < VPT; b0 += BATCH) {
+      float g[BATCH][8], m[BATCH][8];
+      bool fast[BATCH];
+#pragma unroll
+      for (int k = 0; k < BATCH; ++k) {
+        const int v = (b0 + k) * NT + tg;
+        const int i = v / VPR, j0 = (v % VPR) * 8;
+        const int64_t pr = (int64_t)r * tile_h + i, pc = (int64_t)c * tile_w + j0;
+        const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
+        fast[k] = i < tile_h && pr < P.h && j0 + 8 <= tile_w && pc + 8 <= P.w && aligned16<DT>(P.grad, og) &&
+                  (!has_mom || aligned16<DT>(P.momentum, om));
+        if (fast[k]) {
+          load8<DT>(P.grad, og, g[k]);
+          if (has_mom) load8<DT>(P.momentum, om, m[k]);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < BATCH; ++k) {
+        const int v = (b0 + k) * NT + tg;
+        const int i = v / VPR, j0 = (v % VPR) * 8;
+        const int64_t pr = (int64_t)r * tile_h + i, pc = (int64_t)c * tile_w + j0;
+        const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
+        float x[8];
+        if (fast[k]) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = momentum_elem<DT>(g[k][e], &m[k][e], mu, nesterov, has_mom);
+          if (has_mom) store8<DT>(P.momentum, om, m[k]);
+        } else {
+          const bool row_ok = i < tile_h && pr < P.h;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            x[e] = 0.f;
+            if (row_ok && j0 + e < tile_w && pc + e < P.w) {
+              const float gv = load_elem<DT>(P.grad, og + e);
+              float mv = has_mom ? load_elem<DT>(P.momentum, om + e) : 0.f;
+              x[e] = momentum_elem<DT>(gv, &mv, mu, nesterov, has_mom);
+              if (has_mom) store_elem<DT>(P.momentum, om + e, mv);
+            }
+          }
+        }
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          h[e] = f32_to_bf16(x[e]);
+          const float f = bf16_to_f32(h[e]);
+          ssq = fmaf(f, f, ssq);
+        }
+        *reinterpret_cast<lds_u32x4*>(X + lds_pos(i, j0 >> 3, XCH)) =
+            u32x4_t{pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])};
+      }
+    }
+    // ---- normaliser (the gather's block sum, then tile_scale) --------------------
+    const float sum = block_sum<NT>(ssq, red);
+    if (tid == 0) s_inv = 1.0f / (sqrtf(0.f + sum) + eps);
+    __syncthreads();
+    const float inv = s_inv;
+    const int ts = opaque_lane(tid);
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const int v = k * NT + ts;
+      lds_u32x4* const px = reinterpret_cast<lds_u32x4*>(X + lds_pos(v / VPR, v % VPR, XCH));
+      *px = scale8(*px, inv);
+    }
+    __syncthreads();
+
+    ns_iterations<1>(X, A, lane, steps, ca, cb, cc, round_once);
+
+    // ---- untile with WD/LR (the fused untile) ------------------------------------
+    // (the descriptor is looked up again rather than held through the NS
+    // iterations, whose registers it would take)
+    int64_t tu64 = t;
+    asm volatile("" : "+s"(tu64));
+    const HimuonParamDesc& U = params[find_param(params, n_params, tu64)];
+    const int64_t ltu = tu64 - U.tile0;
+    const int ru = (int)(ltu / U.C), cu = (int)(ltu % U.C);
+    const float sc = U.upd_scale;
+    const int tu = opaque_lane(tid);
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const int v = k * NT + tu;
+      const int i = v / VPR, j0 = (v % VPR) * 8;
+      const int64_t pr = (int64_t)ru * tile_h + i, pc = (int64_t)cu * tile_w + j0;
+      if (i < tile_h && j0 < tile_w && pr < U.h && pc < U.w) {
+        const u32x4_t w = *reinterpret_cast<lds_cu32x4*>(X + lds_pos(i, v % VPR, XCH));
+        float y[8];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          y[2 * e2] = sc * bf16_to_f32(w[e2] & 0xffffu);
+          y[2 * e2 + 1] = sc * __uint_as_float(w[e2] & 0xffff0000u);
+        }
+        const int64_t ou = pr * U.ld_upd + pc;
+        const bool full = j0 + 8 <= tile_w && pc + 8 <= U.w && aligned16<PDT>(U.update, ou);
+        const int valid = (int)min<int64_t>(min(8, tile_w - j0), U.w - pc);
+        put8<true, PDT>(U, ou, y, full, valid, sa);
+      }
     }
   }
 }
@@ -396,6 +560,31 @@ int num_cus() {
 }
 
 }  // namespace
+
+bool lds_step_supported(int tile_h, int tile_w, int dtype, int param_dtype) {
+  return tile_h > 0 && tile_h <= tile_w && tile_w <= M &&
+         (dtype == HIMUON_DTYPE_F32 || dtype == HIMUON_DTYPE_BF16) &&
+         (param_dtype == HIMUON_DTYPE_F32 || param_dtype == HIMUON_DTYPE_BF16);
+}
+
+void lds_step_run(const HimuonParamDesc* params, int n_params, int64_t tile_begin, int64_t cnt, int tile_h,
+                  int tile_w, int dtype, int param_dtype, int steps, float a, float b, float c, float eps,
+                  bool round_once, const float* sa, hipStream_t s) {
+  const int64_t wgs = std::min<int64_t>(cnt, (int64_t)3 * 4 * num_cus());
+  const dim3 grid((unsigned)wgs), block(NT);
+  const int ro = round_once ? 1 : 0;
+#define HM_LDS_STEP(D, PD)                                                                                  \
+  hipLaunchKernelGGL((lds_step_kernel<D, PD>), grid, block, 0, s, params, n_params, tile_begin, cnt, tile_h, \
+                     tile_w, steps, a, b, c, eps, ro, sa)
+  if (dtype == HIMUON_DTYPE_F32) {
+    if (param_dtype == HIMUON_DTYPE_F32) HM_LDS_STEP(HIMUON_DTYPE_F32, HIMUON_DTYPE_F32);
+    else HM_LDS_STEP(HIMUON_DTYPE_F32, HIMUON_DTYPE_BF16);
+  } else {
+    if (param_dtype == HIMUON_DTYPE_F32) HM_LDS_STEP(HIMUON_DTYPE_BF16, HIMUON_DTYPE_F32);
+    else HM_LDS_STEP(HIMUON_DTYPE_BF16, HIMUON_DTYPE_BF16);
+  }
+#undef HM_LDS_STEP
+}
 
 bool ns5_lds_supported(int mp, int np) { return mp == M && (np == 128 || np == 256 || np == 512); }
 

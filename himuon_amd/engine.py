@@ -166,6 +166,21 @@ class TileGroup:
             workspace, sub_batch, round_once=self.round_once,
         )
 
+    def lds_step_ok(self) -> bool:
+        """True when the whole step of this group runs as one launch per chunk
+        (himuon_lds_step): fused mode, 128 x 128 NS tiles without transpose,
+        fp32/bf16 grads and parameters."""
+        return self.fused and nat.lds_step_supported(self.tile_h, self.tile_w, self.dtype, self.upd_dtype)
+
+    def lds_step(self, start: int, count: int, steps: int, scale_alpha: torch.Tensor) -> None:
+        """Momentum, gather, normaliser, NS and the untile with the WD/LR of
+        scale_alpha for tiles start .. start + count - 1, one launch; the tile
+        buffers are not used."""
+        if count <= 0:
+            return
+        nat.lds_step(self.desc, len(self.tile0), start, count, self.tile_h, self.tile_w, self.dtype,
+                     self.upd_dtype, steps, scale_alpha, round_once=self.round_once)
+
     def result(self, steps: int) -> torch.Tensor:
         """Buffer holding the NS output after `steps` iterations."""
         return self.tiles if steps % 2 == 0 else self.alt

@@ -65,6 +65,10 @@ class HiMuon(Optimizer):
     # when their parameters allow it; False keeps update tensors and the
     # separate WD/LR pass for every bucket (same parameters, bit for bit).
     _fuse_untile: bool = True
+    # Such buckets on 128 x 128 NS tiles run the whole step (momentum to
+    # WD/LR) as one LDS-resident launch per chunk (himuon_lds_step); False
+    # keeps the gather / NS / untile launches (same results, bit for bit).
+    _fuse_lds_step: bool = True
 
     def __init__(
         self,
@@ -714,14 +718,19 @@ class HiMuon(Optimizer):
         total_B = 0
         for g in groups:
             grp: TileGroup = g["tiles"]
-            grp.gather()
+            lds = self._fuse_lds_step and grp.lds_step_ok()
+            if not lds:
+                grp.gather()
             ofs = 0
             for c in g["chunks"]:
                 if use_events:
                     ev0 = torch.cuda.Event(enable_timing=True)
                     ev1 = torch.cuda.Event(enable_timing=True)
                     ev0.record()
-                grp.ns(ofs, c, g["steps"], self._workspace, g["sub_batch"])
+                if lds:
+                    grp.lds_step(ofs, c, g["steps"], self._lrwd)
+                else:
+                    grp.ns(ofs, c, g["steps"], self._workspace, g["sub_batch"])
                 if use_events:
                     ev1.record()
                     ev_pairs.append((ev0, ev1))
@@ -729,10 +738,12 @@ class HiMuon(Optimizer):
                 total_B += c
                 ofs += c
             if grp.fused:
-                # WD/LR applied by the untile itself, from the (scale, alpha)
-                # table written before this step; the graph path still lists
-                # the parameters as pending (without an update tensor).
-                grp.untile(g["steps"], self._lrwd)
+                # WD/LR applied by the untile itself (or by the LDS-resident
+                # step), from the (scale, alpha) table written before this
+                # step; the graph path still lists the parameters as pending
+                # (without an update tensor).
+                if not lds:
+                    grp.untile(g["steps"], self._lrwd)
                 if self._in_graph_region:
                     for (p, _), gi in zip(g["entries"], g["group_idx"]):
                         self._pending_updates.append((p, None, gi))

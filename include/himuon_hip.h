@@ -214,6 +214,28 @@ int himuon_ba_bmm_add(const uint16_t* a, const uint16_t* x, uint16_t* out,
                       float gamma, int flags, void* stream);
 
 /*
+ * The whole step of a bucket whose NS tiles are 128 x 128 (tile_h <= tile_w
+ * <= 128, so no tile is transposed) in one launch: for bucket tiles
+ * tile_begin .. tile_begin + n_tiles - 1, himuon_momentum_gather,
+ * himuon_tile_scale, himuon_ns5_ex (flags: HIMUON_NS_ROUND_ONCE only) and
+ * himuon_untile_apply, with each tile held in one workgroup's LDS from the
+ * momentum update to the parameter update. Replaces the per-bucket sequence
+ * of himuon.py:704-719 (momentum, tiling), 232-284 (NS5) and 315-348 (untile,
+ * WD/LR) for small tiles (the reference's one-kernel ns5_smem regime,
+ * himuon.py:263-284). params_dev is the descriptor table of
+ * himuon_momentum_gather / himuon_untile_apply (`update` = the parameter);
+ * dtype (grads and momentum) and param_dtype are each HIMUON_DTYPE_F32 or
+ * HIMUON_DTYPE_BF16. The momentum buffers and parameters end bit-identical to
+ * those four calls; no NS tile buffer is read or written. Other geometries
+ * and dtypes are an argument error.
+ */
+int himuon_lds_step(const HimuonParamDesc* params_dev, int n_params,
+                    int64_t tile_begin, int64_t n_tiles, int tile_h,
+                    int tile_w, int dtype, int param_dtype, int steps,
+                    float a, float b, float c, float eps, int flags,
+                    const float* scale_alpha_dev, void* stream);
+
+/*
  * himuon_ns5_ex without a workspace argument, for callers that cannot
  * allocate (code under hipGraph capture, tight serving loops, harnesses that
  * forbid hipMalloc). No counterpart in the reference. It allocates nothing:

@@ -67,3 +67,19 @@ def test_reference_microbenchmark_points():
     # exp_ns_kernel_microbench.py:279: B = 32, 128, 512, 2048 at T = 128
     assert sorted(bench.NS_MICRO_B.values()) == [32, 128, 512, 2048]
     assert set(bench.NS_MICRO_REF_MS) == set(bench.NS_MICRO_B.values())
+
+
+def test_tile_elements_counts_covered_parameter_elements():
+    from types import SimpleNamespace
+
+    shapes = [(300, 200), (128, 128), (77, 130)]
+    th = tw = 128
+    counts = [(-(-h // th)) * (-(-w // tw)) for h, w in shapes]
+    tile0 = [sum(counts[:i]) for i in range(len(counts))]
+    grp = SimpleNamespace(params=[SimpleNamespace(shape=s) for s in shapes], tile0=tile0, tile_counts=counts,
+                          tile_h=th, tile_w=tw)
+    n_all = sum(counts)
+    assert bench._tile_elements(grp, n_all) == sum(h * w for h, w in shapes)
+    # the first tile row of the 300 x 200 matrix: 128 x 128 + 128 x 72
+    assert bench._tile_elements(grp, 2) == 128 * 128 + 128 * 72
+    assert bench._tile_elements(grp, 0) == 0

@@ -167,6 +167,14 @@ def test_ns5_ex_and_stage_argument_errors(lib):
     assert lib.himuon_ba_bmm_add(8, 16, 24, 1, 512, 512, 1.0, 1.0, 1.0, 1, z) == -22
     assert lib.himuon_ba_bmm_add(8, 16, 24, (1 << 29) + 1, 512, 512, 1.0, 1.0, 1.0, 0, z) == -22
     assert lib.himuon_ba_bmm_add(8, 16, 24, 0, 512, 512, 1.0, 1.0, 1.0, 0x10, z) == 0
+    # the LDS-resident step: tile_h <= tile_w <= 128, fp32/bf16 grads and parameters,
+    # a descriptor table and a (scale, alpha) table, round-once the only flag
+    def lds(prm=8, npar=1, base=0, n=0, th=128, tw=128, dt=0, pdt=1, steps=5, flags=0x10, sa=16):
+        return lib.himuon_lds_step(prm, npar, base, n, th, tw, dt, pdt, steps, 1.0, 1.0, 1.0, 1e-7, flags, sa, z)
+    assert lds() == 0 and lds(th=64, tw=100, dt=1, pdt=0, steps=0) == 0  # empty work: no launch
+    for bad in (dict(th=256), dict(tw=256), dict(th=100, tw=64), dict(dt=2), dict(pdt=2), dict(steps=-1),
+                dict(flags=1), dict(prm=z), dict(npar=0), dict(sa=z), dict(base=-1), dict(n=-1), dict(th=0)):
+        assert lds(**bad) == -22, bad
 
 
 def test_geometry_helpers():

@@ -18,6 +18,11 @@ and checks, with the grads copied to the host where the oracle needs them:
 * the parameters of the sampled tiles after the last replay bit-exact against
   oracle.apply_update of the sampled NS tile (WD/LR fused in the untile).
 
+cfg5's 128 x 128-tile bucket runs the whole step in LDS (himuon_lds_step) and
+stores no NS result: its check is the parameters of the sampled tiles against
+oracle.apply_update of torch's NS5 of the same inputs (tests/test_gpu_lds_step.py
+pins that kernel bit for bit against the separate launches).
+
 Full-matrix groups (cfg3) compare against the 2-D third product of the
 reference (torch.addmm, himuon.py:249-253). cfg5 runs the tile-128 regime,
 then reconfigure(tile_size=512) and the same sequence again (recapture).
@@ -80,8 +85,12 @@ def _check_group(opt, gi, sample, n_steps, p_before, round_once=False, label="")
     same-dtype NS5, momentum region bit-exact, band, fused-untile parameters."""
     g = opt._groups[gi]
     grp = g["tiles"]
+    # 128 x 128-tile buckets run the whole step in LDS (himuon_lds_step): no
+    # NS result is stored, the parameters are the output checked
+    no_tiles = opt._fuse_lds_step and grp.lds_step_ok()
     res = grp.result(g["steps"])
-    assert torch.isfinite(res.float()).all(), f"{label}: non-finite NS output"
+    if not no_tiles:
+        assert torch.isfinite(res.float()).all(), f"{label}: non-finite NS output"
     th, tw, m, n = grp.tile_h, grp.tile_w, grp.m, grp.n
     inputs, outs = [], []
     for t in sample:
@@ -96,6 +105,11 @@ def _check_group(opt, gi, sample, n_steps, p_before, round_once=False, label="")
         outs.append(out.transpose(0, 1) if grp.trans else out)
     X = torch.stack(inputs).to("cuda")
     ref = ns5_torch_staged(X, steps=g["steps"], round_once=round_once)
+    if no_tiles:
+        print(f"  {label}: step in LDS: {len(sample)} tiles' parameters vs torch NS5 + oracle WD/LR", flush=True)
+        assert torch.isfinite(ref).all()
+        _check_params(grp, sample, ref.float(), p_before, label)
+        return
     got = torch.stack(outs).float()
     err = per_tile_rel_fro(got, ref.float())
     print(f"  {label}: {len(sample)} tiles vs torch NS5: max {err.max():.2e} "
@@ -111,14 +125,20 @@ def _check_group(opt, gi, sample, n_steps, p_before, round_once=False, label="")
         lo, hi = O.quintic_band(max(sin.min(), floor), sin.max())
         assert sv.max() <= hi + 0.03
         assert (sv < lo - 0.03).sum() <= int((sin < floor).sum())
-    # parameters of the sampled tiles: WD/LR applied by the fused untile
+    _check_params(grp, sample, got, p_before, label)
+
+
+def _check_params(grp, sample, x, p_before, label):
+    """Parameters of the sampled tiles (WD/LR applied by the fused untile)
+    bit-exact against oracle.apply_update of the NS tiles x (per sample)."""
+    th, tw = grp.tile_h, grp.tile_w
     if grp.fused and p_before is not None:
         pdt = "bfloat16" if grp.params[0].dtype == torch.bfloat16 else "float32"
         scale = np.float32(grp.upd_scales[0])
         for k, t in enumerate(sample):
             i, r, c = _locate(grp, t)
             p = grp.params[i]
-            u = got[k].cpu().numpy()[: min(th, p.shape[0] - r * th), : min(tw, p.shape[1] - c * tw)]
+            u = x[k].cpu().numpy()[: min(th, p.shape[0] - r * th), : min(tw, p.shape[1] - c * tw)]
             upd = O.round_to(O.round_to(u, "float32") * scale, "float32")
             exp = O.apply_update(p_before[t], upd, LR, WD, pdt, "float32")
             now = p.data[r * th : r * th + u.shape[0], c * tw : c * tw + u.shape[1]].float().cpu().numpy()

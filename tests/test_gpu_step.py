@@ -145,7 +145,7 @@ def test_update_tensor_matches_oracle_per_tile():
 
 @pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("cuda_graph", [False, True])
-@pytest.mark.parametrize("tile", [256, (512, 256), 512])
+@pytest.mark.parametrize("tile", [256, (512, 256), 512, 128])
 def test_fused_untile_apply_matches_unfused(pdt, cuda_graph, tile):
     """The fused untile (WD/LR applied in place, inside the graph) leaves the
     parameters bit-identical to the unfused path (update tensors, then the
@@ -183,7 +183,10 @@ def test_fused_untile_apply_matches_unfused(pdt, cuda_graph, tile):
             o.step()
     assert all(g["tiles"].fused for g in o_f._groups)
     assert not any(g["tiles"].fused for g in o_u._groups)
-    assert any(g["tiles"].tile_h > g["tiles"].tile_w for g in o_f._groups)  # transposed untile ran
+    if tile != 128:  # (at 128 every matrix is tiled: no tall whole-matrix group)
+        assert any(g["tiles"].tile_h > g["tiles"].tile_w for g in o_f._groups)  # transposed untile ran
+    # 128 x 128 NS tiles of fp32/bf16 parameters: the whole step ran in LDS
+    assert any(g["tiles"].lds_step_ok() for g in o_f._groups) == (tile == 128 and pdt != torch.float16)
     if cuda_graph:
         assert o_f._cuda_graph is not None and o_f._pending_updates
         assert all(u is None for _, u, _ in o_f._pending_updates)
@@ -198,14 +201,16 @@ def test_fused_untile_apply_matches_unfused(pdt, cuda_graph, tile):
     if pdt == torch.float16:
         # torch's fp16 p.add_(u, alpha=-lr) is p + alpha*u as one fp32 fma (the form
         # the kernels use) in its vectorised bulk path, measured bit for bit on the
-        # GPU, but not in the non-vectorised tail of each launch, which rounds some
+        # GPU, but not in the non-vectorised tail of each launch (the last
+        # partial block, up to a few thousand elements), which rounds some
         # elements differently by 1 ulp. The tail covers the same elements every
         # step, so over 7 steps those drift by a few ulp. Against torch's ops (the
         # referee, and the unfused path's eager warm-up steps): at most 0.1 % of
-        # the elements, by at most 1e-3 (parameters ~0.05).
+        # the elements plus 100 (a small matrix is mostly tail), by at most 1e-3
+        # (parameters ~0.05).
         for name, m in (("fused", m_f), ("unfused", m_u)):
             for i, shape, n_bad, n, dmax in diffs(m, m_r):
-                assert n_bad <= 1e-3 * n and dmax <= 1e-3, (name, i, shape, n_bad, dmax)
+                assert n_bad <= 1e-3 * n + 100 and dmax <= 1e-3, (name, i, shape, n_bad, dmax)
         return
     bad = [("fused",) + d for d in diffs(m_f, m_r)] + [("unfused",) + d for d in diffs(m_u, m_r)]
     assert not bad, bad
