@@ -77,8 +77,9 @@ PEAK_HBM_GBS = 8000.0
 KERNEL_TRAFFIC = {
     # 4096 tiles: FETCH_SIZE 5,047,199 KiB x 1.99970, WRITE_SIZE 2,097,152 KiB x 1.0
     ("qwen3-4b", "ns_ba_kernel"): (1.2483e+10, "7286bf56a90e560a"),
-    # 65,536 tiles of 128 x 128: FETCH_SIZE 1,050,805 KiB x 1.99982, WRITE_SIZE 2,097,152 KiB x 1.0
-    ("llama3-8b-t128", "ns5_lds_kernel"): (4.2993e+09, "d558f65c98164c2e"),
+    # 65,536 tiles of 128 x 128, the whole step (fp32 grads, momentum and params):
+    # FETCH_SIZE 6,291,797 KiB x 1.99981, WRITE_SIZE 8,389,386 KiB x 1.0
+    ("llama3-8b-t128", "lds_step_kernel"): (2.1475e+10, "f816436dfde488b5"),
 }
 KERNEL_SOURCES = {
     "ns_ba_kernel": ["ns5_ba.hip", "ns5_kernels.h", "common.h"],

@@ -407,7 +407,9 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint
 // iterations and the untile with WD/LR (the fused untile's arithmetic), with
 // the tile held in LDS from the momentum to the parameter update. HBM sees the
 // grad, the momentum buffer (read and written) and the parameter (read and
-// written) once each; no NS tile buffer exists.
+// written) once each; no NS tile buffer exists. A workgroup walks its tiles
+// with the untile of one tile and the gather of its next tile in one pass, so
+// that their memory latencies overlap.
 //
 // Bit-identical to gather -> tile_scale -> NS5 -> untile_apply: every element
 // is computed by the same per-element code, and the tile's sum of squares is
@@ -415,80 +417,123 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint
 // 8-element vectors t, t + 256, ..., t + 1792 of the 128 x 128 tile, each in
 // element order; then the same wave and block reductions, and the same
 // 1 / (sqrt(s) + eps)).
-template <int DT, int PDT>
-__global__ __launch_bounds__(NT, 3) void lds_step_kernel(const HimuonParamDesc* __restrict__ params, int n_params,
-                                                         int64_t tile_begin, int64_t ntiles, int tile_h,
-                                                         int tile_w, int steps, float ca, float cb, float cc,
-                                                         float eps, int round_once,
-                                                         const float* __restrict__ sa) {
-  constexpr int N = 128, XCH = N / 8, VPR = N / 8;  // 16 vectors of 8 per NS row
-  constexpr int VPT = M * VPR / NT;                  // vectors per thread (8)
-  constexpr int BATCH = 2;                           // vectors loaded before any is used
-  __shared__ __attribute__((aligned(16))) uint8_t sx_raw[M * N * 2];
-  __shared__ __attribute__((aligned(16))) uint8_t sa_raw[TRI_BYTES];
-  __shared__ float red[NT / 64];
-  __shared__ float s_inv;
-  lds_u8* const X = (lds_u8*)sx_raw;
-  lds_u8* const A = (lds_u8*)sa_raw;
-  const int tid = threadIdx.x, lane = tid & 63;
+constexpr int SV_N = 128, SV_VPR = SV_N / 8;  // 16 vectors of 8 per NS row
+constexpr int SV_VPT = M * SV_VPR / NT;       // vectors per thread (8)
+constexpr int SV_BATCH = 2;                   // vectors loaded before any is used
 
-  for (int64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
-    const int64_t t = tile_begin + tt;
-    __syncthreads();  // the previous tile's untile reads of X are done
-    const HimuonParamDesc& P = params[find_param(params, n_params, t)];
-    const int64_t lt = t - P.tile0;
-    const int r = (int)(lt / P.C), c = (int)(lt % P.C);
-    const bool has_mom = P.momentum != nullptr;
-    const float mu = P.mu;
-    const bool nesterov = P.nesterov != 0;
+struct TileAt {
+  const HimuonParamDesc* P;
+  int r, c;
+};
 
-    // ---- momentum + bf16(e) + sum of squares (the gather) ----------------------
-    // (thread-dependent addresses from an opaque copy of the thread index in
-    // each phase: hoisted out of the tile loop they would not fit beside the
-    // NS iterations' registers)
-    const int tg = opaque_lane(tid);
-    float ssq = 0.f;
-    // bf16(e) goes to LDS as it is formed; the normaliser is applied in
-    // place once the tile's sum is known (each thread rescales its own
-    // vectors)
+HM_DEV TileAt tile_at(const HimuonParamDesc* __restrict__ params, int n_params, int64_t t) {
+  const HimuonParamDesc* P = params + find_param(params, n_params, t);
+  const int64_t lt = t - P->tile0;
+  return TileAt{P, (int)(lt / P->C), (int)(lt % P->C)};
+}
+
+// UNT: untile with WD/LR of tile tu from X (X' of the NS iterations). GAT:
+// momentum and gather of tile tg into X (bf16(e), not yet normalised);
+// returns this thread's sum of squares of it. Each thread reads and writes
+// only its own vectors v = k NT + tid of X, the same ones in both parts.
+template <int DT, int PDT, bool UNT, bool GAT>
+HM_DEV float step_io(const HimuonParamDesc* __restrict__ params, int n_params, lds_u8* X, int64_t tu, int64_t tg,
+                     int tile_h, int tile_w, const float* __restrict__ sa) {
+#pragma clang fp contract(off)
+  constexpr int XCH = SV_N / 8;
+  TileAt U{nullptr, 0, 0}, G{nullptr, 0, 0};
+  float s = 0.f, alpha = 0.f, sc = 0.f, mu = 0.f;
+  bool has_mom = false, nesterov = false;
+  if constexpr (UNT) {
+    U = tile_at(params, n_params, tu);
+    s = sa[2 * U.P->group];
+    alpha = sa[2 * U.P->group + 1];
+    sc = U.P->upd_scale;
+  }
+  if constexpr (GAT) {
+    G = tile_at(params, n_params, tg);
+    has_mom = G.P->momentum != nullptr;
+    mu = G.P->mu;
+    nesterov = G.P->nesterov != 0;
+  }
+  // (addresses from an opaque copy of the thread index: hoisted out of the
+  // tile loop they would not fit beside the NS iterations' registers)
+  const int tq = opaque_lane((int)threadIdx.x);
+  float ssq = 0.f;
 #pragma unroll 1
-    for (int b0 = 0; b0 < VPT; b0 += BATCH) {
-      float g[BATCH][8], m[BATCH][8];
-      bool fast[BATCH];
+  for (int b0 = 0; b0 < SV_VPT; b0 += SV_BATCH) {
+    // phase 1: every global load of the batch (parameters of tile tu, grads
+    // and momentum of tile tg) before any is used
+    float pv[SV_BATCH][8], g[SV_BATCH][8], m[SV_BATCH][8];
+    bool uok[SV_BATCH], ufull[SV_BATCH], fast[SV_BATCH];
 #pragma unroll
-      for (int k = 0; k < BATCH; ++k) {
-        const int v = (b0 + k) * NT + tg;
-        const int i = v / VPR, j0 = (v % VPR) * 8;
-        const int64_t pr = (int64_t)r * tile_h + i, pc = (int64_t)c * tile_w + j0;
-        const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
-        fast[k] = i < tile_h && pr < P.h && j0 + 8 <= tile_w && pc + 8 <= P.w && aligned16<DT>(P.grad, og) &&
-                  (!has_mom || aligned16<DT>(P.momentum, om));
+    for (int k = 0; k < SV_BATCH; ++k) {
+      const int v = (b0 + k) * NT + tq;
+      const int i = v / SV_VPR, j0 = (v % SV_VPR) * 8;
+      if constexpr (UNT) {
+        const int64_t pr = (int64_t)U.r * tile_h + i, pc = (int64_t)U.c * tile_w + j0;
+        const int64_t ou = pr * U.P->ld_upd + pc;
+        uok[k] = i < tile_h && j0 < tile_w && pr < U.P->h && pc < U.P->w;
+        ufull[k] = uok[k] && j0 + 8 <= tile_w && pc + 8 <= U.P->w && aligned16<PDT>(U.P->update, ou);
+        if (ufull[k]) load8<PDT>(U.P->update, ou, pv[k]);
+      }
+      if constexpr (GAT) {
+        const int64_t pr = (int64_t)G.r * tile_h + i, pc = (int64_t)G.c * tile_w + j0;
+        const int64_t og = pr * G.P->ld_grad + pc, om = pr * G.P->ld_mom + pc;
+        fast[k] = i < tile_h && pr < G.P->h && j0 + 8 <= tile_w && pc + 8 <= G.P->w &&
+                  aligned16<DT>(G.P->grad, og) && (!has_mom || aligned16<DT>(G.P->momentum, om));
         if (fast[k]) {
-          load8<DT>(P.grad, og, g[k]);
-          if (has_mom) load8<DT>(P.momentum, om, m[k]);
+          load8<DT>(G.P->grad, og, g[k]);
+          if (has_mom) load8<DT>(G.P->momentum, om, m[k]);
         }
       }
+    }
+    // phase 2: the untile reads X' of vector v, then the gather overwrites it
 #pragma unroll
-      for (int k = 0; k < BATCH; ++k) {
-        const int v = (b0 + k) * NT + tg;
-        const int i = v / VPR, j0 = (v % VPR) * 8;
-        const int64_t pr = (int64_t)r * tile_h + i, pc = (int64_t)c * tile_w + j0;
-        const int64_t og = pr * P.ld_grad + pc, om = pr * P.ld_mom + pc;
+    for (int k = 0; k < SV_BATCH; ++k) {
+      const int v = (b0 + k) * NT + tq;
+      const int i = v / SV_VPR, j0 = (v % SV_VPR) * 8;
+      lds_u32x4* const px = reinterpret_cast<lds_u32x4*>(X + lds_pos(i, v % SV_VPR, XCH));
+      if constexpr (UNT) {
+        if (uok[k]) {
+          const u32x4_t w = *px;
+          float y[8];
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            y[2 * e2] = sc * bf16_to_f32(w[e2] & 0xffffu);
+            y[2 * e2 + 1] = sc * __uint_as_float(w[e2] & 0xffff0000u);
+          }
+          const int64_t pr = (int64_t)U.r * tile_h + i, pc = (int64_t)U.c * tile_w + j0;
+          const int64_t ou = pr * U.P->ld_upd + pc;
+          if (ufull[k]) {  // put8<true>'s full form, its load issued above
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              pv[k][e] = __builtin_fmaf(alpha, round_to<PDT>(y[e]), round_to<PDT>(pv[k][e] * s));
+            store8<PDT>(U.P->update, ou, pv[k]);
+          } else {
+            const int valid = (int)min<int64_t>(min(8, tile_w - j0), U.P->w - pc);
+            put8<true, PDT>(*U.P, ou, y, false, valid, sa);
+          }
+        }
+      }
+      if constexpr (GAT) {
+        const int64_t pr = (int64_t)G.r * tile_h + i, pc = (int64_t)G.c * tile_w + j0;
+        const int64_t og = pr * G.P->ld_grad + pc, om = pr * G.P->ld_mom + pc;
         float x[8];
         if (fast[k]) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) x[e] = momentum_elem<DT>(g[k][e], &m[k][e], mu, nesterov, has_mom);
-          if (has_mom) store8<DT>(P.momentum, om, m[k]);
+          if (has_mom) store8<DT>(G.P->momentum, om, m[k]);
         } else {
-          const bool row_ok = i < tile_h && pr < P.h;
+          const bool row_ok = i < tile_h && pr < G.P->h;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             x[e] = 0.f;
-            if (row_ok && j0 + e < tile_w && pc + e < P.w) {
-              const float gv = load_elem<DT>(P.grad, og + e);
-              float mv = has_mom ? load_elem<DT>(P.momentum, om + e) : 0.f;
+            if (row_ok && j0 + e < tile_w && pc + e < G.P->w) {
+              const float gv = load_elem<DT>(G.P->grad, og + e);
+              float mv = has_mom ? load_elem<DT>(G.P->momentum, om + e) : 0.f;
               x[e] = momentum_elem<DT>(gv, &mv, mu, nesterov, has_mom);
-              if (has_mom) store_elem<DT>(P.momentum, om + e, mv);
+              if (has_mom) store_elem<DT>(G.P->momentum, om + e, mv);
             }
           }
         }
@@ -499,54 +544,57 @@ __global__ __launch_bounds__(NT, 3) void lds_step_kernel(const HimuonParamDesc* 
           const float f = bf16_to_f32(h[e]);
           ssq = fmaf(f, f, ssq);
         }
-        *reinterpret_cast<lds_u32x4*>(X + lds_pos(i, j0 >> 3, XCH)) =
-            u32x4_t{pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])};
+        *px = u32x4_t{pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])};
       }
     }
-    // ---- normaliser (the gather's block sum, then tile_scale) --------------------
+  }
+  return ssq;
+}
+
+template <int DT, int PDT>
+__global__ __launch_bounds__(NT, 3) void lds_step_kernel(const HimuonParamDesc* __restrict__ params, int n_params,
+                                                         int64_t tile_begin, int64_t ntiles, int tile_h,
+                                                         int tile_w, int steps, float ca, float cb, float cc,
+                                                         float eps, int round_once,
+                                                         const float* __restrict__ sa) {
+  constexpr int XCH = SV_N / 8;
+  __shared__ __attribute__((aligned(16))) uint8_t sx_raw[M * SV_N * 2];
+  __shared__ __attribute__((aligned(16))) uint8_t sa_raw[TRI_BYTES];
+  __shared__ float red[NT / 64];
+  __shared__ float s_inv;
+  lds_u8* const X = (lds_u8*)sx_raw;
+  lds_u8* const A = (lds_u8*)sa_raw;
+  const int lane = threadIdx.x & 63;
+
+  int64_t tt = blockIdx.x;
+  if (tt >= ntiles) return;
+  float ssq = step_io<DT, PDT, false, true>(params, n_params, X, 0, tile_begin + tt, tile_h, tile_w, sa);
+  for (;;) {
+    // ---- normaliser (the gather's block sum, then tile_scale), X0 in place ------
     const float sum = block_sum<NT>(ssq, red);
-    if (tid == 0) s_inv = 1.0f / (sqrtf(0.f + sum) + eps);
+    if (threadIdx.x == 0) s_inv = 1.0f / (sqrtf(0.f + sum) + eps);
     __syncthreads();
     const float inv = s_inv;
-    const int ts = opaque_lane(tid);
+    const int ts = opaque_lane((int)threadIdx.x);
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) {
+    for (int k = 0; k < SV_VPT; ++k) {
       const int v = k * NT + ts;
-      lds_u32x4* const px = reinterpret_cast<lds_u32x4*>(X + lds_pos(v / VPR, v % VPR, XCH));
+      lds_u32x4* const px = reinterpret_cast<lds_u32x4*>(X + lds_pos(v / SV_VPR, v % SV_VPR, XCH));
       *px = scale8(*px, inv);
     }
     __syncthreads();
 
     ns_iterations<1>(X, A, lane, steps, ca, cb, cc, round_once);
 
-    // ---- untile with WD/LR (the fused untile) ------------------------------------
-    // (the descriptor is looked up again rather than held through the NS
-    // iterations, whose registers it would take)
-    int64_t tu64 = t;
-    asm volatile("" : "+s"(tu64));
-    const HimuonParamDesc& U = params[find_param(params, n_params, tu64)];
-    const int64_t ltu = tu64 - U.tile0;
-    const int ru = (int)(ltu / U.C), cu = (int)(ltu % U.C);
-    const float sc = U.upd_scale;
-    const int tu = opaque_lane(tid);
-#pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-      const int v = k * NT + tu;
-      const int i = v / VPR, j0 = (v % VPR) * 8;
-      const int64_t pr = (int64_t)ru * tile_h + i, pc = (int64_t)cu * tile_w + j0;
-      if (i < tile_h && j0 < tile_w && pr < U.h && pc < U.w) {
-        const u32x4_t w = *reinterpret_cast<lds_cu32x4*>(X + lds_pos(i, v % VPR, XCH));
-        float y[8];
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          y[2 * e2] = sc * bf16_to_f32(w[e2] & 0xffffu);
-          y[2 * e2 + 1] = sc * __uint_as_float(w[e2] & 0xffff0000u);
-        }
-        const int64_t ou = pr * U.ld_upd + pc;
-        const bool full = j0 + 8 <= tile_w && pc + 8 <= U.w && aligned16<PDT>(U.update, ou);
-        const int valid = (int)min<int64_t>(min(8, tile_w - j0), U.w - pc);
-        put8<true, PDT>(U, ou, y, full, valid, sa);
-      }
+    // ---- untile with WD/LR of this tile, gather of the next -----------------------
+    const int64_t nx = tt + gridDim.x;
+    if (nx < ntiles) {
+      ssq = step_io<DT, PDT, true, true>(params, n_params, X, tile_begin + tt, tile_begin + nx, tile_h, tile_w,
+                                         sa);
+      tt = nx;
+    } else {
+      step_io<DT, PDT, true, false>(params, n_params, X, tile_begin + tt, 0, tile_h, tile_w, sa);
+      break;
     }
   }
 }

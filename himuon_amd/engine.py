@@ -84,17 +84,43 @@ class TileGroup:
         self.tile0 = [sum(counts[:i]) for i in range(len(counts))]
         self.n_tiles = sum(counts)
         self.ppt = nat.gather_partials_per_tile(self.tile_h, self.tile_w, self.mp, self.np)
-        shape = (self.n_tiles, self.mp, self.np)
-        # X ping-pongs between tiles and alt through the NS iterations.
-        self.tiles = torch.empty(shape, device=device, dtype=torch.bfloat16)
-        self.alt = torch.empty(shape, device=device, dtype=torch.bfloat16)
-        self.partials = torch.empty((self.n_tiles, self.ppt), device=device, dtype=torch.float32)
-        self.inv = torch.empty((self.n_tiles,), device=device, dtype=torch.float32)
+        # NS tile buffers, allocated on first use: a group whose step runs in
+        # LDS (lds_step) never needs them.
+        self._bufs = None
         self.updates = [] if self.fused else [torch.empty(g.shape, device=device, dtype=self.upd_dtype) for g in grads]
         self.upd_scales = list(upd_scales)
         self._sig = None
         self.desc = None
         self.bind(grads, moms, mus, nesterovs)
+
+    # -- NS tile buffers ------------------------------------------------------
+    def _buffers(self):
+        if self._bufs is None:
+            shape = (self.n_tiles, self.mp, self.np)
+            # X ping-pongs between tiles and alt through the NS iterations.
+            self._bufs = (
+                torch.empty(shape, device=self.device, dtype=torch.bfloat16),
+                torch.empty(shape, device=self.device, dtype=torch.bfloat16),
+                torch.empty((self.n_tiles, self.ppt), device=self.device, dtype=torch.float32),
+                torch.empty((self.n_tiles,), device=self.device, dtype=torch.float32),
+            )
+        return self._bufs
+
+    @property
+    def tiles(self) -> torch.Tensor:
+        return self._buffers()[0]
+
+    @property
+    def alt(self) -> torch.Tensor:
+        return self._buffers()[1]
+
+    @property
+    def partials(self) -> torch.Tensor:
+        return self._buffers()[2]
+
+    @property
+    def inv(self) -> torch.Tensor:
+        return self._buffers()[3]
 
     # -- descriptors -----------------------------------------------------
     @staticmethod

@@ -541,7 +541,9 @@ class HiMuon(Optimizer):
                 upd_dtype=update_dtype(params, dtype),
                 apply_groups=gidx if fusable(params, gidx, dtype) else None,
             )
-            self._concat_buffers[bucket["bucket_key"]] = grp.tiles
+            if not (self._fuse_lds_step and grp.lds_step_ok()):
+                # (a bucket whose step runs in LDS has no NS tile buffer)
+                self._concat_buffers[bucket["bucket_key"]] = grp.tiles
             out.append(
                 {
                     "tiles": grp,
