@@ -9,56 +9,60 @@
 // instead of A in, B out, B and X in and X' out (2.5 MiB). The first product
 // (A = bf16(X X^T)) stays the streamed Gram kernel (ns5_stream.hip).
 //
-// Work item (tile t, panel p), rows i0 = 128 p .. i0 + 127, four waves; wave
-// w owns output columns 128 w .. 128 w + 127 in both stages, as 4 x 4
-// v_mfma_f32_32x32x16_bf16 tiles (256 fp32 accumulators per lane, one wave
-// per SIMD). Items are spread persistently, a contiguous range per XCD.
+// Work item (tile t, panel p), rows i0 = 128 p .. i0 + 127, eight waves, two
+// per SIMD: wave w = 4 h + c owns output columns col0 = 128 c + 64 h ..
+// + 63 in both stages, as 2 x 4 v_mfma_f32_32x32x16_bf16 tiles (128 fp32
+// accumulators per lane), so that while one wave of a SIMD waits on a read
+// or works through an epilogue the other's MFMAs issue. Items are spread
+// persistently, a contiguous range per XCD.
 //
 //  Stage 1: B_P[i][j] = bf16(c sum_k A[i0+i][k] A[j][k] + b A[i0+i][j]).
 //    Row-side operand A_P (128 x 512 bf16 = 128 KiB) resident in LDS region
 //    R, loaded with direct-to-LDS DMA during the previous item's stage 2, a
 //    quarter at a time as soon as every wave has read the B_P columns it
 //    replaces. Column-side operand: A is exactly symmetric, so A[j][k] =
-//    A[k][j] and the wave streams rows k of A restricted to its 128 columns.
+//    A[k][j] and the wave streams rows k of A restricted to its 64 columns.
 //  Stage 2: X'_P[i][j] = bf16(bf16(sum_k B_P[i][k] X[k][j]) + a X[i0+i][j]).
 //    Row-side operand B_P, written over A_P in R by the stage-1 epilogue;
 //    column-side operand: rows k of X restricted to the wave's columns.
 //
 //  Both K loops run the same schedule: the streamed rows go from global
-//  memory into a four-unit register ring (a unit = 32 rows = two k-steps of
-//  16, 8 x 16-byte loads per lane), three units ahead of the MFMAs; each
-//  k-step's 16 rows are written to one of two wave-private 4 KiB staging
-//  buffers and read back as column fragments with ds_read_b64_tr_b16
-//  (contraction along the rows). No workgroup barrier inside a loop: the
-//  staging buffers are private and a wave's LDS operations execute in order.
-//  After stage 2 the ring carries the X_P rows i0 .. i0 + 127 (the a X term).
+//  memory into a four-unit register ring (a unit = 32 rows x 64 columns =
+//  two k-steps of 16, 4 x 16-byte loads per lane), three units ahead of the
+//  MFMAs; each k-step's 16 rows are written to one of two wave-private
+//  2 KiB staging buffers and read back as column fragments with
+//  ds_read_b64_tr_b16 (contraction along the rows). No workgroup barrier
+//  inside a loop: the staging buffers are private and a wave's LDS
+//  operations execute in order. After stage 2 the ring carries the X_P rows
+//  i0 .. i0 + 127 (the a X term).
 //
 //  Stage-1 epilogue: B_P = bf16(c acc + b A_P) for the wave's own columns,
 //  read from and written to the same R addresses, between two barriers.
 //  Stage-2 epilogue, per 32-row block: X_P into the accumulator layout
-//  through the wave's 8 KiB staging area, the result back through it into
-//  256-byte row stores, and the next item's first ring units loaded.
+//  through the wave's 4 KiB area, the result back through it into 128-byte
+//  row stores, and the next item's first ring units loaded.
 //
 // Per item the waves meet at barriers: A_P landed, A_P reads done, B_P
 // written, a quarter of B_P read (three times inside stage 2), all of B_P
-// read. Each output
-// element sums its k terms in one fp32 accumulator in ascending k with the
-// same MFMA as the three-kernel path, so results are bit-identical to it.
+// read. Each output element sums its k terms in one fp32 accumulator in
+// ascending k with the same MFMA as the three-kernel path, so results are
+// bit-identical to it.
 //
-// LDS: R (128 KiB, 8-row blocks, below), then a 8 KiB area per wave (two
-// 4 KiB staging buffers: 16 rows x 256 B, chunk c of row r at c ^ 4 (r % 4),
-// conflict-free for row writes and transposing reads; epilogue: 32 rows x
-// 256 B, chunk c of row r at c ^ (r % 16)).
+// LDS: R (128 KiB, 8-row blocks, below), then a 4 KiB area per wave: two
+// 2 KiB staging buffers (16 rows x 128 B, 16-byte chunk c of row r at
+// c ^ 4 ((r / 2) % 2), conflict-free for the row writes and the transposing
+// reads); in the epilogue one block of 32 rows x 128 B, chunk c of row r at
+// c ^ (r / 2) % 8.
 #include "ns5_kernels.h"
 
 namespace {
 
 constexpr int T = 512;           // tile edge (mp = np)
 constexpr int P = 128;           // panel rows
-constexpr int NW = 4;            // waves
+constexpr int NW = 8;            // waves, two per SIMD
 constexpr int NTH = 64 * NW;
 constexpr int R_BYTES = P * T * 2;          // 128 KiB
-constexpr int WAREA = 8192;                 // per-wave staging
+constexpr int WAREA = 4096;                 // per-wave staging
 constexpr int LDS_BYTES = R_BYTES + NW * WAREA;
 constexpr int NKS = T / 16;                 // k-steps per stage
 constexpr int NUNIT = T / 32;               // ring units per stage (2 k-steps each)
@@ -94,9 +98,9 @@ HM_DEV void gstore16(uint16_t* base, uint32_t off, u32x4_t v) {
   *reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(base) + off) = v;
 }
 
-// One ring unit: 8 x 16 bytes per lane.
+// One ring unit: 4 x 16 bytes per lane (32 rows x 64 columns per wave).
 struct Unit {
-  u32x4_t v[8];
+  u32x4_t v[4];
 };
 
 // Region R holds a 128 x 512 panel (A_P, then B_P) in 1 KiB blocks of 8 rows
@@ -114,14 +118,15 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[LDS_BYTES];
   lds_u8* const lds = (lds_u8*)lds_raw;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col0 = 128 * (wave & 3) + 64 * (wave >> 2);  // the wave's first output column
   const int l32 = lane & 31, hi = lane >> 5;
   const uint32_t r_base = (uint32_t)(uintptr_t)lds;
   // R row fragments: fragment (ti, ks) of lane l (row 32 ti + l32, chunk
   // 2 (ks % 4) + hi of block column ks / 4) is at a per-k-step lane base
   // plus the immediate 32 KiB ti. The chunk term is made opaque per k-step,
-  // so that the four bases are formed where they are used (two VALU
-  // operations) instead of being held through the K loops.
+  // so that the bases are formed where they are used (two VALU operations)
+  // instead of being held through the K loops.
   const int rl_row = 8192 * (l32 >> 3) + 128 * (l32 & 7);
   const int rl_sw = hi ^ r_swz(l32);
   auto rfrag_base = [&](int ks) -> const lds_u8* {
@@ -130,16 +135,17 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     return lds + rl_row + 16 * ((2 * (ks & 3)) ^ sw) + 1024 * (ks >> 2);
   };
   lds_u8* const W = lds + R_BYTES + wave * WAREA;
-  // Row staging: two 4 KiB buffers (k-steps ks % 2), 16 rows x 256 bytes,
-  // 16-byte chunk c of row r at c ^ 4 (r % 4) (conflict-free for the row
-  // writes and the transposing reads). Row writes: lane base xw + 1 KiB n;
-  // transposing reads of column fragment tj: lane base xr[tj] (+ 1 KiB for
-  // k-rows 4..7 of the lane's eight).
-  lds_u8* const xw = W + 256 * (lane >> 4) + (((lane & 15) ^ (4 * (lane >> 4))) << 4);
-  const int tr_m = (lane & 15) >> 2;
-  const lds_u8* const xr0 = W + 256 * (8 * hi + tr_m) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3);
-  // epilogue staging (32 rows x 256 B, chunk c of row r at c ^ (r & 15))
-  auto ep_off = [](int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); };
+  // Row writes: lane l writes row 8 n + l / 8 (n = 0, 1), chunk l % 8.
+  const int wr = lane >> 3;
+  lds_u8* const xw = W + 128 * wr + (((lane & 7) ^ (4 * ((wr >> 1) & 1))) << 4);
+  // Transposing reads, 16-lane group i = l % 16: rows 8 hi + i / 4 (+ 4 for
+  // the upper four k), bytes 32 ((l / 16) % 2) + 8 (i % 4) of the tile's
+  // 64-byte segment, which sits at segment t2 ^ (i / 8) % 2 of the row.
+  const int tr_i = lane & 15;
+  const lds_u8* const xr0 = W + 128 * (8 * hi + (tr_i >> 2)) + 32 * ((lane >> 4) & 1) + 8 * (lane & 3);
+  const int tr_s = (tr_i >> 3) & 1;
+  // epilogue block (32 rows x 128 B, chunk c of row r at c ^ (r / 2) % 8)
+  auto ep_off = [](int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); };
 
   // (32-bit item indices: the launcher takes at most 2^29 tiles per call)
   const int total = (int)g.ntiles * (T / P);
@@ -150,34 +156,28 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
   int item = ibeg + (int)(blockIdx.x >> 3);
   if (item >= iend) return;
 
-  // ---- operand sources ----------------------------------------------------------
-  // Both stages stream k-rows of a 512 x 512 bf16 matrix restricted to the
-  // wave's 128 columns: stage 1 rows of A (A is exactly symmetric, so its
-  // row k holds column k: A[k][j] = A[j][k], the B-operand of c A_P A^T),
-  // stage 2 rows of X. A ring unit is 32 rows: lane l holds row row0 + 4 n +
-  // l / 16, columns 128 w + 8 (l % 16) .. + 7, in v[n] (n = 0..7). The uniform
-  // part of each address goes into the scalar base, the lane part is one
-  // 32-bit offset (a tile is 512 KiB).
-  const uint32_t x_lane = 2u * ((lane >> 4) * T + 128 * wave + 8 * (lane & 15));
-  auto load_row = [&](const uint16_t* M, int row0, Unit& d, int n) { d.v[n] = gload16(M + (row0 + 4 * n) * T, x_lane); };
+  // Unit of 32 rows restricted to the wave's 64 columns: lane l holds row
+  // row0 + 8 n + l / 8, columns col0 + 8 (l % 8) .. + 7, in v[n].
+  const uint32_t x_lane = 2u * ((lane >> 3) * T + col0 + 8 * (lane & 7));
+  auto load_row = [&](const uint16_t* M, int row0, Unit& d, int n) { d.v[n] = gload16(M + (row0 + 8 * n) * T, x_lane); };
   auto load_rows = [&](const uint16_t* M, int row0, Unit& d) {
 #pragma unroll
-    for (int n = 0; n < 8; ++n) load_row(M, row0, d, n);
+    for (int n = 0; n < 4; ++n) load_row(M, row0, d, n);
   };
   // A_P into R, one block per instruction: lane l lands at row l / 8,
   // position l % 8 and fetches chunk (l % 8) ^ swz(row). Call q (0..3) loads
   // block columns m = 2 q, 2 q + 1 (k-steps 8 q .. 8 q + 7); wave w takes
-  // block rows g = 4 w .. 4 w + 3 (ln, wv: the lane and wave index, opaque
-  // per call so the addresses are formed where they are used).
+  // block rows g = 2 w, 2 w + 1 (ln, wv: the lane and wave index, opaque per
+  // call so the addresses are formed where they are used).
   auto dma_ap = [&](const uint16_t* At, int i0, int q, int ln, int wv) {
 #pragma unroll
-    for (int gg = 0; gg < 4; ++gg) {
-      const int g = 4 * wv + gg;
-      const int rr = ln >> 3;  // row within the block
+    for (int gg = 0; gg < 2; ++gg) {
+      const int gb = 2 * wv + gg;
+      const int rr = ln >> 3;
       const int ch = (ln & 7) ^ rr ^ (gg & 1);
-      const uint16_t* src = At + (i0 + 8 * g + rr) * T + 128 * q + 8 * ch;
+      const uint16_t* src = At + (i0 + 8 * gb + rr) * T + 128 * q + 8 * ch;
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) dma16(src + 64 * mm, r_base + 1024 * (8 * g + 2 * q + mm));
+      for (int mm = 0; mm < 2; ++mm) dma16(src + 64 * mm, r_base + 1024 * (8 * gb + 2 * q + mm));
     }
   };
 
@@ -212,50 +212,47 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     float xs = 1.f;
     if constexpr (SC) xs = g.xinv[tile];
 
-    // A_P landed: the 24 ring loads of units 0..2 were issued after its DMA.
-    wait_vm<3 * 8>();
+    // A_P landed: the ring loads of units 0..2 (and the stores between them)
+    // were issued after its DMA.
+    wait_vm<3 * 4>();
     lds_barrier();
 
-    f32x16_t acc[4][4];
+    f32x16_t acc[2][4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
 
     // ---- one K loop: acc += P_frag x (rows of M) over k = 0..511 ----------------------
-    // k-step ks: its 16 rows (ring unit ks / 2, registers 4 (ks % 2) ..) go to
+    // k-step ks: its 16 rows (ring unit ks / 2, registers 2 (ks % 2) ..) go to
     // staging buffer ks % 2 and come back as column fragments through
     // transposing reads; the row fragments of the panel (A_P or B_P) come from
-    // R. While k-step ks's four MFMA rows run: after rows 0..2, k-step ks + 1's
-    // reads (the R fragments first, every MFMA row needs them; then the
-    // transposing reads); after row 3, k-step ks + 2's rows into buffer ks % 2,
-    // behind those reads (a wave's LDS operations execute in order); after
-    // each row, one load of the unit three ahead.
-    u32x4_t fa[2][4], fb[2][4];
-    auto read_frags = [&](int ks, int b, int part) {
-      const int buf = 4096 * (ks & 1);
-      if (part == 0) {
-        const lds_u8* const rb = rfrag_base(ks);
+    // R. After the first MFMA row of k-step ks, all of k-step ks + 1's reads;
+    // after the second, k-step ks + 2's rows into buffer ks % 2, behind those
+    // reads (a wave's LDS operations execute in order); after each row, one
+    // load of the unit three ahead.
+    u32x4_t fa[2][2], fb[2][4];
+    auto read_frags = [&](int ks, int b) {
+      const lds_u8* const rb = rfrag_base(ks);
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) fb[b][ti] = *reinterpret_cast<const lds_u32x4*>(rb + 32768 * ti);
-      } else {
+      for (int ti = 0; ti < 4; ++ti) fb[b][ti] = *reinterpret_cast<const lds_u32x4*>(rb + 32768 * ti);
+      const int buf = 2048 * (ks & 1);
 #pragma unroll
-        for (int t2 = 2 * (part - 1); t2 < 2 * (part - 1) + 2; ++t2) {
-          const lds_u8* p = xr0 + buf + ((t2 ^ tr_m) << 6);
-          const u32x2_t lo = read_tr(p);
-          const u32x2_t up = read_tr(p + 1024);
-          fa[b][t2] = u32x4_t{lo[0], lo[1], up[0], up[1]};
-        }
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const lds_u8* p = xr0 + buf + ((t2 ^ tr_s) << 6);
+        const u32x2_t lo = read_tr(p);
+        const u32x2_t up = read_tr(p + 512);
+        fa[b][t2] = u32x4_t{lo[0], lo[1], up[0], up[1]};
       }
     };
     auto write_rows = [&](int ks, const Unit& su, bool xrows) {
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        u32x4_t v = su.v[4 * (ks & 1) + n];
+      for (int n = 0; n < 2; ++n) {
+        u32x4_t v = su.v[2 * (ks & 1) + n];
         if (SC && xrows) v = scale8_rne(v, xs);
-        *reinterpret_cast<lds_u32x4*>(xw + 4096 * (ks & 1) + 1024 * n) = v;
+        *reinterpret_cast<lds_u32x4*>(xw + 2048 * (ks & 1) + 1024 * n) = v;
       }
     };
     // stream unit v of this item: stage-1 A rows (v < 16), stage-2 X rows
@@ -265,11 +262,10 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
       row0 = v < NUNIT ? 32 * v : v < 2 * NUNIT ? 32 * (v - NUNIT) : i0 + 32 * (v - 2 * NUNIT);
     };
     auto kloop = [&](int base) {  // base: stream index of the stage's unit 0 (0 or 16)
-      const bool xrows = base == NUNIT;  // stage 2 streams X
+      const bool xrows = base == NUNIT;
       write_rows(0, ring[base % NSLOT], xrows);
       write_rows(1, ring[base % NSLOT], xrows);
-#pragma unroll
-      for (int p = 0; p < 3; ++p) read_frags(0, 0, p);
+      read_frags(0, 0);
 #pragma unroll
       for (int u = 0; u < NUNIT; ++u) {
         const uint16_t* M;
@@ -281,18 +277,17 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
           const int ks = 2 * u + s;
           const int b = (s + 1) & 1;
 #pragma unroll
-          for (int tj = 0; tj < 4; ++tj) {
+          for (int ti = 0; ti < 4; ++ti) acc[0][ti] = mfma(fa[s][0], fb[s][ti], acc[0][ti]);
+          __builtin_amdgcn_sched_barrier(0);
+          if (ks + 1 < NKS) read_frags(ks + 1, b);
+          load_row(M, row0, dst, 2 * s);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int ti = 0; ti < 4; ++ti) acc[tj][ti] = mfma(fa[s][tj], fb[s][ti], acc[tj][ti]);
-            __builtin_amdgcn_sched_barrier(0);
-            if (tj < 3) {
-              if (ks + 1 < NKS) read_frags(ks + 1, b, tj);
-            } else if (ks + 2 < NKS) {
-              write_rows(ks + 2, ring[(base + u + 1) % NSLOT], xrows);  // unit u + 1, half s
-            }
-            load_row(M, row0, dst, 4 * s + tj);
-            __builtin_amdgcn_sched_barrier(0);
-          }
+          for (int ti = 0; ti < 4; ++ti) acc[1][ti] = mfma(fa[s][1], fb[s][ti], acc[1][ti]);
+          __builtin_amdgcn_sched_barrier(0);
+          if (ks + 2 < NKS) write_rows(ks + 2, ring[(base + u + 1) % NSLOT], xrows);
+          load_row(M, row0, dst, 2 * s + 1);
+          __builtin_amdgcn_sched_barrier(0);
           // Stage 2, after k-step 8 q + 7 (q < 3): every wave has consumed
           // the B_P fragments of k-steps up to 8 q + 7 (block columns 2 q,
           // 2 q + 1; the reads in flight are of k-step 8 q + 8), so after a
@@ -311,27 +306,24 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     kloop(0);
 
     // ---- stage-1 epilogue: B_P = bf16(c acc + b A_P) over A_P, own columns ----------
-    // element (i = 32 ti + l32, j = 128 w + 32 tj + 8 q + 4 hi + e): block
-    // (4 ti + l32 / 8, 2 w + tj / 2), row l32 % 8, chunk 4 (tj % 2) + q, bytes
-    // 8 hi ..
+    // element (i = 32 ti + l32, j = col0 + 32 tj + 8 q + 4 hi + e): block
+    // (4 ti + l32 / 8, col0 / 64), row l32 % 8, chunk 4 tj + q, bytes 8 hi ..
     lds_barrier();  // every wave is done reading A_P fragments
     {
       const int el = lane_o & 31, esw = r_swz(el);
-      lds_u8* const ep1 = lds + 8192 * (el >> 3) + 2048 * wave + 128 * (el & 7) + 8 * (lane_o >> 5);
-      auto ep1_off = [&](int ti, int tj, int q) {
-        return 32768 * ti + 1024 * (tj >> 1) + 16 * ((4 * (tj & 1) + q) ^ esw);
-      };
+      lds_u8* const ep1 = lds + 8192 * (el >> 3) + 1024 * (col0 >> 6) + 128 * (el & 7) + 8 * (lane_o >> 5);
+      auto ep1_off = [&](int ti, int tj, int q) { return 32768 * ti + 16 * ((4 * tj + q) ^ esw); };
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) {
-        // all 16 A_P pieces of this row block first, one wait, then B_P over them
-        u32x2_t av[4][4];
+        // all 8 A_P pieces of this row block first, one wait, then B_P over them
+        u32x2_t av[2][4];
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
+        for (int tj = 0; tj < 2; ++tj)
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             av[tj][q] = *reinterpret_cast<const lds_cu32x2*>(ep1 + ep1_off(ti, tj, q));
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
+        for (int tj = 0; tj < 2; ++tj)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             float y[4];
@@ -346,7 +338,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     lds_barrier();  // B_P complete
 
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b)
 #pragma unroll
@@ -366,22 +358,22 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
 
     // ---- stage-2 epilogue -------------------------------------------------------------
     // X_P unit q (rows 32 q ..) sits in ring[(2 NUNIT + q) % NSLOT] = ring[q].
-    const int el32 = lane_o & 31, ehi = lane_o >> 5, erow = lane_o >> 4, ech = lane_o & 15;
+    const int el32 = lane_o & 31, ehi = lane_o >> 5, erow = lane_o >> 3, ech = lane_o & 7;
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       const Unit& xp = ring[(2 * NUNIT + ti) % NSLOT];
 #pragma unroll
-      for (int n = 0; n < 8; ++n)
-        *reinterpret_cast<lds_u32x4*>(W + ep_off(4 * n + erow, ech)) = SC ? scale8_rne(xp.v[n], xs) : xp.v[n];
-      // X_P in the accumulator layout: all 16 pieces, one wait
-      u32x2_t xv[4][4];
+      for (int n = 0; n < 4; ++n)
+        *reinterpret_cast<lds_u32x4*>(W + ep_off(8 * n + erow, ech)) = SC ? scale8_rne(xp.v[n], xs) : xp.v[n];
+      // X_P in the accumulator layout: all 8 pieces, one wait
+      u32x2_t xv[2][4];
 #pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
+      for (int tj = 0; tj < 2; ++tj)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           xv[tj][q] = *reinterpret_cast<const lds_cu32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi);
 #pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
+      for (int tj = 0; tj < 2; ++tj)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           float y[4], bx[4];
@@ -402,12 +394,12 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
           *reinterpret_cast<lds_u32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi) =
               u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
         }
-      // the 32 result rows: all 8 row reads, one wait, 8 row stores
-      u32x4_t rows[8];
+      // the 32 result rows: all 4 row reads, one wait, 4 row stores
+      u32x4_t rows[4];
 #pragma unroll
-      for (int n = 0; n < 8; ++n) rows[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(4 * n + erow, ech));
+      for (int n = 0; n < 4; ++n) rows[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
 #pragma unroll
-      for (int n = 0; n < 8; ++n) gstore16(Yt + (i0 + 32 * ti + 4 * n) * T, xl_o, rows[n]);
+      for (int n = 0; n < 4; ++n) gstore16(Yt + (i0 + 32 * ti + 8 * n) * T, xl_o, rows[n]);
       // the next item's stage-1 units 0..2 into the slots X_P units 0..2 freed
       if (more && ti < AHEAD) load_rows(nAt, 32 * ti, ring[ti]);
     }
