@@ -139,6 +139,26 @@ def test_fused_ba_bmm_add_equals_the_two_stages(round_once):
         assert torch.equal(fused, ref)
 
 
+@pytest.mark.parametrize("n", [1, 3, 65, 257, 2049])
+def test_fused_ba_bmm_add_tile_counts(n):
+    """The fused kernel's persistent item walk (4 panels per tile, a
+    contiguous item range per XCD, 32 workgroups per XCD) at tile counts that
+    leave XCDs idle (1, 3), end ranges mid-tile and mid-walk (65, 257) and run
+    up to 9 items per workgroup (2049): bit for bit the two-stage result, every
+    tile written (the output starts as NaN)."""
+    print(f"[ba_bmm_add] n={n}", flush=True)
+    X = _normalised(_rand((n, 512, 512), seed=n))
+    A = torch.empty_like(X)
+    nat.xxt(X, A, n, 512, 512)
+    Bm = torch.empty_like(A)
+    nat.ba_plus_caa(A, Bm, n, 512, C_, B_)
+    two = torch.empty_like(X)
+    nat.bmm_add(Bm, X, two, n, 512, 512, A_)
+    fused = torch.full_like(X, float("nan"))
+    nat.ba_bmm_add(A, X, fused, n, C_, B_, A_)
+    assert torch.equal(fused, two)
+
+
 def test_stage_products_compose_to_ns_iteration():
     """One NS iteration as XXT -> ba_plus_cAA -> fused_bmm_add equals
     himuon_ns5 with steps = 1 on the same normalised tiles, bit for bit."""
