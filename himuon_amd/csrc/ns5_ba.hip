@@ -38,9 +38,11 @@
 //
 //  Stage-1 epilogue: B_P = bf16(c acc + b A_P) for the wave's own columns,
 //  read from and written to the same R addresses, between two barriers.
-//  Stage-2 epilogue, per 32-row block: X_P into the accumulator layout
-//  through the wave's 4 KiB area, the result back through it into 128-byte
-//  row stores, and the next item's first ring units loaded.
+//  Stage-2 epilogue, per 32-row block: bf16(B X) through the wave's 4 KiB
+//  area into the row layout of the stores, + a X there with the X_P rows the
+//  ring holds in that layout, 128-byte row stores, and the next item's first
+//  ring units loaded. (The 2-D form rounds B X + a X once: X_P goes into the
+//  accumulator layout through the area instead, and the sum back.)
 //
 // Per item the waves meet at barriers: A_P landed, A_P reads done, B_P
 // written, a quarter of B_P read (three times inside stage 2), all of B_P
@@ -357,47 +359,67 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     if (more) dma_ap(nAt, ni0, 3, lane_o, wave_o);
 
     // ---- stage-2 epilogue -------------------------------------------------------------
-    // X_P unit q (rows 32 q ..) sits in ring[(2 NUNIT + q) % NSLOT] = ring[q].
+    // X_P unit q (rows 32 q ..) sits in ring[(2 NUNIT + q) % NSLOT] = ring[q],
+    // in the row layout of the stores (row 8 n + l / 8, columns 8 (l % 8) ..).
     const int el32 = lane_o & 31, ehi = lane_o >> 5, erow = lane_o >> 3, ech = lane_o & 7;
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       const Unit& xp = ring[(2 * NUNIT + ti) % NSLOT];
-#pragma unroll
-      for (int n = 0; n < 4; ++n)
-        *reinterpret_cast<lds_u32x4*>(W + ep_off(8 * n + erow, ech)) = SC ? scale8_rne(xp.v[n], xs) : xp.v[n];
-      // X_P in the accumulator layout: all 8 pieces, one wait
-      u32x2_t xv[2][4];
-#pragma unroll
-      for (int tj = 0; tj < 2; ++tj)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          xv[tj][q] = *reinterpret_cast<const lds_cu32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi);
-#pragma unroll
-      for (int tj = 0; tj < 2; ++tj)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float y[4], bx[4];
-#pragma unroll
-          for (int e = 0; e < 4; e += 2) {
-            const float v0 = acc[tj][ti][4 * q + e], v1 = acc[tj][ti][4 * q + e + 1];
-            if constexpr (ROUND_ONCE) {
-              bx[e] = v0;
-              bx[e + 1] = v1;
-            } else {  // bf16(B X), two at a time
-              const uint32_t r = pk_bf16(v0, v1);
-              bx[e] = __uint_as_float(r << 16);
-              bx[e + 1] = __uint_as_float(r & 0xffff0000u);
-            }
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = fmaf(ca, bf16_to_f32(half16(xv[tj][q][e >> 1], e & 1)), bx[e]);
-          *reinterpret_cast<lds_u32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi) =
-              u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
-        }
-      // the 32 result rows: all 4 row reads, one wait, 4 row stores
       u32x4_t rows[4];
+      if constexpr (!ROUND_ONCE) {
+        // bf16(B X) through W into the row layout, then + a X there with X_P
+        // straight from the ring: the same operations on the same values as
+        // in the accumulator layout, without staging X_P
 #pragma unroll
-      for (int n = 0; n < 4; ++n) rows[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x16_t& v = acc[tj][ti];
+            *reinterpret_cast<lds_u32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi) =
+                u32x2_t{pk_bf16(v[4 * q], v[4 * q + 1]), pk_bf16(v[4 * q + 2], v[4 * q + 3])};
+          }
+        // all 4 row reads, one wait
+        u32x4_t bxr[4];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) bxr[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const u32x4_t x = SC ? scale8_rne(xp.v[n], xs) : xp.v[n];
+#pragma unroll
+          for (int w2 = 0; w2 < 4; ++w2) {
+            const float y0 = fmaf(ca, __uint_as_float(x[w2] << 16), __uint_as_float(bxr[n][w2] << 16));
+            const float y1 = fmaf(ca, __uint_as_float(x[w2] & 0xffff0000u), __uint_as_float(bxr[n][w2] & 0xffff0000u));
+            rows[n][w2] = pk_bf16(y0, y1);
+          }
+        }
+      } else {
+        // bf16(B X + a X): X_P into the accumulator layout through W, the
+        // fp32 sum there, the result back through W into rows
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+          *reinterpret_cast<lds_u32x4*>(W + ep_off(8 * n + erow, ech)) = SC ? scale8_rne(xp.v[n], xs) : xp.v[n];
+        // X_P in the accumulator layout: all 8 pieces, one wait
+        u32x2_t xv[2][4];
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            xv[tj][q] = *reinterpret_cast<const lds_cu32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi);
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              y[e] = fmaf(ca, bf16_to_f32(half16(xv[tj][q][e >> 1], e & 1)), acc[tj][ti][4 * q + e]);
+            *reinterpret_cast<lds_u32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi) =
+                u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
+          }
+        // the 32 result rows: all 4 row reads, one wait
+#pragma unroll
+        for (int n = 0; n < 4; ++n) rows[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
+      }
 #pragma unroll
       for (int n = 0; n < 4; ++n) gstore16(Yt + (i0 + 32 * ti + 8 * n) * T, xl_o, rows[n]);
       // the next item's stage-1 units 0..2 into the slots X_P units 0..2 freed
