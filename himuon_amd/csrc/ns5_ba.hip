@@ -289,6 +289,13 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
           __builtin_amdgcn_sched_barrier(0);
           if (ks + 2 < NKS) write_rows(ks + 2, ring[(base + u + 1) % NSLOT], xrows);
           load_row(M, row0, dst, 2 * s + 1);
+          // Stage 2, last unit: the fourth X_P unit (rows i0 + 96 ..) into
+          // the slot stage-2 unit 15 left (staged during unit 14)
+          if (xrows && u == NUNIT - 1) {
+            Unit& x3 = ring[(2 * NUNIT + AHEAD) % NSLOT];
+            load_row(Xt, i0 + 96, x3, 2 * s);
+            load_row(Xt, i0 + 96, x3, 2 * s + 1);
+          }
           __builtin_amdgcn_sched_barrier(0);
           // Stage 2, after k-step 8 q + 7 (q < 3): every wave has consumed
           // the B_P fragments of k-steps up to 8 q + 7 (block columns 2 q,
@@ -348,8 +355,6 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
 
     // ---- stage 2: B_P X ---------------------------------------------------------------
     kloop(NUNIT);
-    // X_P rows i0 + 96 .. i0 + 127 (the fourth X_P unit) into the slot unit 15 freed
-    load_rows(Xt, i0 + 96, ring[(2 * NUNIT + AHEAD) % NSLOT]);
     // All X_P units in before the last quarter of the next A_P's DMA is
     // issued: a wait for an X_P unit after it would also wait for the DMA
     // (vmcnt retires in order).
