@@ -11,17 +11,22 @@
 //   B  = bf16(c (A A^T) + b A)          lower 32x32 tiles only
 //   X' = bf16(bf16(B X) + a X)
 //
-// 256 threads = 4 waves. Gram products: the 10 lower 32x32 tiles (ti >= tj
-// of the 4x4 grid of v_mfma_f32_32x32x16_bf16 tiles) are split 3, 3, 2, 2 over
-// the four waves (GramPart), so every SIMD takes part. A and B are symmetric
+// np = 128: 256 threads = 4 waves, three workgroups per CU; np = 256, 512:
+// 512 threads = 8 waves, two per SIMD (one workgroup fits a CU). Gram
+// products: the 10 lower 32x32 tiles (ti >= tj of the 4x4 grid of
+// v_mfma_f32_32x32x16_bf16 tiles) are split 3, 3, 2, 2 over the four waves
+// (GramPart), or over eight waves with the same 3, 3, 2, 2 per SIMD
+// (GramPart8), so every SIMD takes part. A and B are symmetric
 // and only those 10 tiles are stored (20 KiB): a row fragment of an upper
 // tile (i, k), k > i, is read from the stored tile (k, i) with the
 // contraction along its rows. A diagonal tile is computed whole and is
 // exactly symmetric (element (i, j) and (j, i) sum the same products in the
 // same order), and an off-diagonal tile read transposed holds the values its
 // mirror would, so every operand is the full matrix's, bit for bit. Apply:
-// wave w owns columns w np/4 .. + np/4 - 1 of all 128 rows (in passes of at
-// most 64 columns) and writes X' over its own columns of X as each pass ends.
+// wave w of NW owns columns w np/NW .. + np/NW - 1 of all 128 rows (in passes
+// of at most 64 columns) and writes X' over its own columns of X as each pass
+// ends. Every output element sums its k terms in one accumulator in the same
+// order whatever the wave count, so both forms give the same bits.
 // Products accumulate in registers; B replaces A after a workgroup barrier.
 // X is read as the MFMA B operand with the contraction along its rows through
 // ds_read_b64_tr_b16.
@@ -36,7 +41,7 @@
 // 64-byte rows, chunk ch of row r at ch ^ ((r / 4) % 4): 16 consecutive rows
 // of one chunk and 4 consecutive rows of 2 chunks hit distinct bank groups.
 // np = 128: 52 KiB per workgroup, three workgroups per CU; np = 256: 84 KiB,
-// np = 512: 148 KiB, one per CU.
+// np = 512: 148 KiB, one per CU (eight waves).
 #include "elem_ops.h"
 #include "ns5_kernels.h"
 
@@ -118,6 +123,50 @@ template <> struct GramPart<2> {  // (3,0) (3,1)
 template <> struct GramPart<3> {  // (3,2) (3,3)
   static constexpr int NR = 2, NTL = 2, ROW[3] = {2, 3, 0}, I[3] = {1, 1, 0}, J[3] = {0, 1, 0};
 };
+// The same 10 tiles over eight waves (two per SIMD; wave w shares SIMD w % 4
+// with wave w + 4): the diagonal tiles in pairs, the off-diagonal ones alone,
+// so a SIMD still computes 3, 3, 2, 2 tiles. Each tile sums its k terms in
+// one accumulator in the same order as the four-wave split.
+template <int W> struct GramPart8;
+template <> struct GramPart8<0> {  // (0,0) (1,1)
+  static constexpr int NR = 2, NTL = 2, ROW[3] = {0, 1, 0}, I[3] = {0, 1, 0}, J[3] = {0, 1, 0};
+};
+template <> struct GramPart8<1> {  // (2,2) (3,3)
+  static constexpr int NR = 2, NTL = 2, ROW[3] = {2, 3, 0}, I[3] = {0, 1, 0}, J[3] = {0, 1, 0};
+};
+template <int TI, int TJ> struct GramPartOne {  // (TI, TJ), TI > TJ
+  static constexpr int NR = 2, NTL = 1, ROW[3] = {TI, TJ, 0}, I[3] = {0, 0, 0}, J[3] = {1, 0, 0};
+};
+template <> struct GramPart8<2> : GramPartOne<1, 0> {};
+template <> struct GramPart8<3> : GramPartOne<2, 0> {};
+template <> struct GramPart8<4> : GramPartOne<2, 1> {};
+template <> struct GramPart8<5> : GramPartOne<3, 0> {};
+template <> struct GramPart8<6> : GramPartOne<3, 1> {};
+template <> struct GramPart8<7> : GramPartOne<3, 2> {};
+
+// Calls f(part) with wave `wave`'s share of a Gram product (NW = 4 or 8).
+template <int NW, class F>
+HM_DEV void with_part(int wave, F&& f) {
+  if constexpr (NW == 4) {
+    switch (wave) {
+      case 0: f(GramPart<0>{}); break;
+      case 1: f(GramPart<1>{}); break;
+      case 2: f(GramPart<2>{}); break;
+      default: f(GramPart<3>{}); break;
+    }
+  } else {
+    switch (wave) {
+      case 0: f(GramPart8<0>{}); break;
+      case 1: f(GramPart8<1>{}); break;
+      case 2: f(GramPart8<2>{}); break;
+      case 3: f(GramPart8<3>{}); break;
+      case 4: f(GramPart8<4>{}); break;
+      case 5: f(GramPart8<5>{}); break;
+      case 6: f(GramPart8<6>{}); break;
+      default: f(GramPart8<7>{}); break;
+    }
+  }
+}
 
 // Fragments of row tile R at k-step KS: from X (SCH chunks per row) or, TRI,
 // from a symmetric matrix stored as its lower tiles.
@@ -129,9 +178,8 @@ HM_DEV u32x4_t row_frag(const lds_u8* S, int l32, int hi, int tr_krow, int tr_co
     return *reinterpret_cast<lds_cu32x4*>(S + lds_pos(32 * R + l32, 2 * KS + hi, SCH));
 }
 
-template <int W, bool TRI, int SCH, int KS>
+template <class P, bool TRI, int SCH, int KS>
 HM_DEV void gram_step(const lds_u8* S, int l32, int hi, int tr_krow, int tr_col, f32x16_t (&acc)[3]) {
-  using P = GramPart<W>;
   u32x4_t f[P::NR];
   f[0] = row_frag<TRI, SCH, P::ROW[0], KS>(S, l32, hi, tr_krow, tr_col);
   f[1] = row_frag<TRI, SCH, P::ROW[1], KS>(S, l32, hi, tr_krow, tr_col);
@@ -140,33 +188,31 @@ HM_DEV void gram_step(const lds_u8* S, int l32, int hi, int tr_krow, int tr_col,
   for (int k = 0; k < P::NTL; ++k) acc[k] = mfma(f[P::J[k]], f[P::I[k]], acc[k]);
 }
 
-template <int W, bool TRI, int SCH, int... KS>
+template <class P, bool TRI, int SCH, int... KS>
 HM_DEV void gram_steps(const lds_u8* S, int l32, int hi, int tr_krow, int tr_col, f32x16_t (&acc)[3],
                        std::integer_sequence<int, KS...>) {
-  (gram_step<W, TRI, SCH, KS>(S, l32, hi, tr_krow, tr_col, acc), ...);
+  (gram_step<P, TRI, SCH, KS>(S, l32, hi, tr_krow, tr_col, acc), ...);
 }
 
 // acc[k] = (S S^T) tile k of wave W, S = LDS operand with SCH chunks per row
 // and K = 8 SCH columns (TRI: a symmetric 128 x 128 matrix stored as its
 // lower tiles). Lane holds element 4 q + e of acc[k] at
 // C[32 ROW[I[k]] + l32][32 ROW[J[k]] + 8 q + 4 hi + e].
-template <int W, bool TRI, int SCH>
+template <class P, bool TRI, int SCH>
 HM_DEV void gram_mma(const lds_u8* S, int lane, f32x16_t (&acc)[3]) {
-  using P = GramPart<W>;
   const int ln = opaque_lane(lane), l32 = ln & 31, hi = ln >> 5;
   const int tr_krow = tr_krow_of(ln), tr_col = tr_col_of(ln);
 #pragma unroll
   for (int k = 0; k < P::NTL; ++k)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[k][e] = 0.f;
-  gram_steps<W, TRI, SCH>(S, l32, hi, tr_krow, tr_col, acc, std::make_integer_sequence<int, SCH / 2>{});
+  gram_steps<P, TRI, SCH>(S, l32, hi, tr_krow, tr_col, acc, std::make_integer_sequence<int, SCH / 2>{});
 }
 
 // Store wave W's bf16 tiles o[k][q] (q: 4 columns each) as lower tiles of
 // the symmetric matrix C.
-template <int W>
+template <class P>
 HM_DEV void gram_store(lds_u8* C, int lane, const u32x2_t (&o)[3][4]) {
-  using P = GramPart<W>;
   const int ln = opaque_lane(lane), l32 = ln & 31, hi = ln >> 5;
 #pragma unroll
   for (int k = 0; k < P::NTL; ++k) {
@@ -178,27 +224,26 @@ HM_DEV void gram_store(lds_u8* C, int lane, const u32x2_t (&o)[3][4]) {
 }
 
 // A = bf16(X X^T): wave W's tiles into A.
-template <int W, int XCH>
+template <class P, int XCH>
 HM_DEV void gram_a(const lds_u8* X, lds_u8* A, int lane) {
   f32x16_t acc[3];
-  gram_mma<W, false, XCH>(X, lane, acc);
+  gram_mma<P, false, XCH>(X, lane, acc);
   u32x2_t o[3][4];
 #pragma unroll
-  for (int k = 0; k < GramPart<W>::NTL; ++k)
+  for (int k = 0; k < P::NTL; ++k)
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       o[k][q] = u32x2_t{pk_bf16(acc[k][4 * q], acc[k][4 * q + 1]), pk_bf16(acc[k][4 * q + 2], acc[k][4 * q + 3])};
-  gram_store<W>(A, lane, o);
+  gram_store<P>(A, lane, o);
 }
 
 // B = bf16(c (A A^T) + b A) for wave W's tiles, into registers (A is still
 // read by the other waves; the caller stores after a barrier).
-template <int W>
+template <class P>
 HM_DEV void gram_b(const lds_u8* A, int lane, float cb, float cc, u32x2_t (&o)[3][4]) {
-  using P = GramPart<W>;
   constexpr int ACH = M / 8;
   f32x16_t acc[3];
-  gram_mma<W, true, ACH>(A, lane, acc);
+  gram_mma<P, true, ACH>(A, lane, acc);
   const int ln = opaque_lane(lane), l32 = ln & 31, hi = ln >> 5;
 #pragma unroll
   for (int k = 0; k < P::NTL; ++k) {
@@ -253,47 +298,35 @@ HM_DEV void apply_steps(const lds_u8* B, const lds_u8* X, int jb, int lane, f32x
 // `steps` NS iterations on the tile X0 in LDS (X, 128 x 128 NQ), A/B in the
 // lower-tile buffer A; X' replaces X. Every thread of the workgroup calls it;
 // it ends with a workgroup barrier.
-template <int NQ>
+template <int NQ, int NW>
 HM_DEV void ns_iterations(lds_u8* X, lds_u8* A, int lane, int steps, float ca, float cb, float cc,
                           int round_once) {
   constexpr int N = 128 * NQ;
   constexpr int XCH = N / 8;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar branches
   for (int it = 0; it < steps; ++it) {
     // ---- A = bf16(X X^T) ------------------------------------------------------
-    switch (wave) {
-      case 0: gram_a<0, XCH>(X, A, lane); break;
-      case 1: gram_a<1, XCH>(X, A, lane); break;
-      case 2: gram_a<2, XCH>(X, A, lane); break;
-      default: gram_a<3, XCH>(X, A, lane); break;
-    }
+    with_part<NW>(wave, [&](auto part) { gram_a<decltype(part), XCH>(X, A, lane); });
     __syncthreads();
 
     // ---- B = bf16(c (A A^T) + b A), in place of A --------------------------------
-    {
+    // (one dispatch on the wave-uniform index for the product, the barrier and
+    // the store, so each wave's B tiles stay in registers across the barrier;
+    // every wave reaches exactly one of the barriers)
+    with_part<NW>(wave, [&](auto part) {
       u32x2_t o[3][4];
-      switch (wave) {
-        case 0: gram_b<0>(A, lane, cb, cc, o); break;
-        case 1: gram_b<1>(A, lane, cb, cc, o); break;
-        case 2: gram_b<2>(A, lane, cb, cc, o); break;
-        default: gram_b<3>(A, lane, cb, cc, o); break;
-      }
+      gram_b<decltype(part)>(A, lane, cb, cc, o);
       __syncthreads();  // every read of A (products and the b A term) is done
-      switch (wave) {
-        case 0: gram_store<0>(A, lane, o); break;
-        case 1: gram_store<1>(A, lane, o); break;
-        case 2: gram_store<2>(A, lane, o); break;
-        default: gram_store<3>(A, lane, o); break;
-      }
-    }
+      gram_store<decltype(part)>(A, lane, o);
+    });
     __syncthreads();
 
     // ---- X' = bf16(bf16(B X) + a X), in place of X ------------------------------
-    // Wave w owns columns w np/4 .. + np/4 - 1 over all 128 rows, in passes of
-    // at most 64 columns. It reads only its own columns of X, so it
+    // Wave w owns columns w np/NW .. + np/NW - 1 over all 128 rows, in passes
+    // of at most 64 columns. It reads only its own columns of X, so it
     // overwrites them as each pass ends, without waiting for the other waves.
     {
-      constexpr int WCOL = N / 4;                 // columns per wave
+      constexpr int WCOL = N / NW;                // columns per wave
       constexpr int PT = WCOL >= 64 ? 2 : 1;      // 32-column tiles per pass
 #pragma unroll 1
       for (int pass = 0; pass < WCOL / (32 * PT); ++pass) {
@@ -342,8 +375,14 @@ HM_DEV void ns_iterations(lds_u8* X, lds_u8* A, int lane, int steps, float ca, f
   }
 }
 
+// Threads per workgroup: 128 x 128 tiles run three 4-wave workgroups per CU;
+// wider tiles (84 or 148 KiB of LDS, one workgroup per CU) run eight waves,
+// two per SIMD.
 template <int NQ>
-__global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint16_t* x,
+constexpr int lds_threads() { return NQ == 1 ? NT : 2 * NT; }
+
+template <int NQ, int NTQ = lds_threads<NQ>()>
+__global__ __launch_bounds__(NTQ, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint16_t* x,
                                                         uint16_t* out,
                                                         const float* __restrict__ inv,
                                                         int64_t ntiles, int steps, float ca,
@@ -358,7 +397,7 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
 
-  constexpr int VPT = M * XCH / NT;  // 16-byte chunks per thread
+  constexpr int VPT = M * XCH / NTQ;  // 16-byte chunks per thread
   // np = 256 (one workgroup per CU) loads the next tile during this tile's
   // iterations; np = 128 (three per CU) leaves the load latency to the other
   // workgroups and keeps the registers; np = 512 has no registers to spare
@@ -369,7 +408,7 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint
     const uint16_t* src = x + t * (int64_t)M * N;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-      const int idx = k * NT + tid;
+      const int idx = k * NTQ + tid;
       v[k] = *reinterpret_cast<const u32x4_t*>(src + (int64_t)(idx / XCH) * N + (idx % XCH) * 8);
     }
   };
@@ -381,20 +420,20 @@ __global__ __launch_bounds__(NT, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uint
     __syncthreads();  // the previous tile's final LDS reads are done
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-      const int idx = k * NT + tid;
+      const int idx = k * NTQ + tid;
       *reinterpret_cast<lds_u32x4*>(X + lds_pos(idx / XCH, idx % XCH, XCH)) = scale8(v[k], sc);
     }
     // the next tile's loads run under this tile's iterations
     if (PREFETCH && t + gridDim.x < ntiles) load_tile(t + gridDim.x);
     __syncthreads();
 
-    ns_iterations<NQ>(X, A, lane, steps, ca, cb, cc, round_once);
+    ns_iterations<NQ, NTQ / 64>(X, A, lane, steps, ca, cb, cc, round_once);
 
     // ---- result -> global ----------------------------------------------------------
     uint16_t* dst = out + t * (int64_t)M * N;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-      const int idx = k * NT + tid;
+      const int idx = k * NTQ + tid;
       *reinterpret_cast<u32x4_t*>(dst + (int64_t)(idx / XCH) * N + (idx % XCH) * 8) =
           *reinterpret_cast<lds_cu32x4*>(X + lds_pos(idx / XCH, idx % XCH, XCH));
     }
@@ -584,7 +623,7 @@ __global__ __launch_bounds__(NT, 3) void lds_step_kernel(const HimuonParamDesc* 
     }
     __syncthreads();
 
-    ns_iterations<1>(X, A, lane, steps, ca, cb, cc, round_once);
+    ns_iterations<1, 4>(X, A, lane, steps, ca, cb, cc, round_once);
 
     // ---- untile with WD/LR of this tile, gather of the next -----------------------
     const int64_t nx = tt + gridDim.x;
@@ -642,9 +681,9 @@ void ns5_lds_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp
   uint16_t* out = (steps & 1) ? y : x;
   const int64_t wgs = std::min<int64_t>(cnt, (int64_t)(np == 128 ? 3 : 1) * 4 * num_cus());
   if (np == 128)
-    hipLaunchKernelGGL(ns5_lds_kernel<1>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
+    hipLaunchKernelGGL(ns5_lds_kernel<1>, dim3((unsigned)wgs), dim3(lds_threads<1>()), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
   else if (np == 256)
-    hipLaunchKernelGGL(ns5_lds_kernel<2>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
+    hipLaunchKernelGGL(ns5_lds_kernel<2>, dim3((unsigned)wgs), dim3(lds_threads<2>()), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
   else
-    hipLaunchKernelGGL(ns5_lds_kernel<4>, dim3((unsigned)wgs), dim3(NT), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
+    hipLaunchKernelGGL(ns5_lds_kernel<4>, dim3((unsigned)wgs), dim3(lds_threads<4>()), 0, s, x, out, inv, cnt, steps, a, b, c, round_once ? 1 : 0);
 }
