@@ -446,9 +446,11 @@ __global__ __launch_bounds__(NTQ, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uin
 // iterations and the untile with WD/LR (the fused untile's arithmetic), with
 // the tile held in LDS from the momentum to the parameter update. HBM sees the
 // grad, the momentum buffer (read and written) and the parameter (read and
-// written) once each; no NS tile buffer exists. A workgroup walks its tiles
-// with the untile of one tile and the gather of its next tile in one pass, so
-// that their memory latencies overlap.
+// written) once each; no NS tile buffer exists. One tile per workgroup: the
+// workgroups that start as others finish fall out of step with each other, so
+// a CU's three workgroups are mostly in different phases (memory or NS). That
+// measured faster than persistent workgroups that walk several tiles, even
+// with one tile's untile and the next one's gather merged into one pass.
 //
 // Bit-identical to gather -> tile_scale -> NS5 -> untile_apply: every element
 // is computed by the same per-element code, and the tile's sum of squares is
@@ -471,14 +473,15 @@ HM_DEV TileAt tile_at(const HimuonParamDesc* __restrict__ params, int n_params, 
   return TileAt{P, (int)(lt / P->C), (int)(lt % P->C)};
 }
 
-// UNT: untile with WD/LR of tile tu from X (X' of the NS iterations). GAT:
-// momentum and gather of tile tg into X (bf16(e), not yet normalised);
-// returns this thread's sum of squares of it. Each thread reads and writes
-// only its own vectors v = k NT + tid of X, the same ones in both parts.
+// Exactly one of UNT and GAT. UNT: untile with WD/LR of tile tu from X (X'
+// of the NS iterations). GAT: momentum and gather of tile tg into X (bf16(e),
+// not yet normalised); returns this thread's sum of squares of it. Each
+// thread reads and writes only its own vectors v = k NT + tid of X.
 template <int DT, int PDT, bool UNT, bool GAT>
 HM_DEV float step_io(const HimuonParamDesc* __restrict__ params, int n_params, lds_u8* X, int64_t tu, int64_t tg,
                      int tile_h, int tile_w, const float* __restrict__ sa) {
 #pragma clang fp contract(off)
+  static_assert(UNT != GAT, "one tile pass per call");
   constexpr int XCH = SV_N / 8;
   TileAt U{nullptr, 0, 0}, G{nullptr, 0, 0};
   float s = 0.f, alpha = 0.f, sc = 0.f, mu = 0.f;
@@ -495,14 +498,15 @@ HM_DEV float step_io(const HimuonParamDesc* __restrict__ params, int n_params, l
     mu = G.P->mu;
     nesterov = G.P->nesterov != 0;
   }
-  // (addresses from an opaque copy of the thread index: hoisted out of the
-  // tile loop they would not fit beside the NS iterations' registers)
+  // (addresses from an opaque copy of the thread index: shared with the other
+  // pass and kept live across the NS iterations they would not fit beside
+  // those iterations' registers)
   const int tq = opaque_lane((int)threadIdx.x);
   float ssq = 0.f;
 #pragma unroll 1
   for (int b0 = 0; b0 < SV_VPT; b0 += SV_BATCH) {
-    // phase 1: every global load of the batch (parameters of tile tu, grads
-    // and momentum of tile tg) before any is used
+    // phase 1: every global load of the batch (parameters of tile tu, or
+    // grads and momentum of tile tg) before any is used
     float pv[SV_BATCH][8], g[SV_BATCH][8], m[SV_BATCH][8];
     bool uok[SV_BATCH], ufull[SV_BATCH], fast[SV_BATCH];
 #pragma unroll
@@ -527,7 +531,7 @@ HM_DEV float step_io(const HimuonParamDesc* __restrict__ params, int n_params, l
         }
       }
     }
-    // phase 2: the untile reads X' of vector v, then the gather overwrites it
+    // phase 2: the untile reads X' of vector v, or the gather writes it
 #pragma unroll
     for (int k = 0; k < SV_BATCH; ++k) {
       const int v = (b0 + k) * NT + tq;
@@ -605,37 +609,27 @@ __global__ __launch_bounds__(NT, 3) void lds_step_kernel(const HimuonParamDesc* 
   lds_u8* const A = (lds_u8*)sa_raw;
   const int lane = threadIdx.x & 63;
 
-  int64_t tt = blockIdx.x;
+  const int64_t tt = blockIdx.x;  // the grid has one workgroup per tile
   if (tt >= ntiles) return;
-  float ssq = step_io<DT, PDT, false, true>(params, n_params, X, 0, tile_begin + tt, tile_h, tile_w, sa);
-  for (;;) {
-    // ---- normaliser (the gather's block sum, then tile_scale), X0 in place ------
-    const float sum = block_sum<NT>(ssq, red);
-    if (threadIdx.x == 0) s_inv = 1.0f / (sqrtf(0.f + sum) + eps);
-    __syncthreads();
-    const float inv = s_inv;
-    const int ts = opaque_lane((int)threadIdx.x);
+  const float ssq = step_io<DT, PDT, false, true>(params, n_params, X, 0, tile_begin + tt, tile_h, tile_w, sa);
+  // ---- normaliser (the gather's block sum, then tile_scale), X0 in place ----------
+  const float sum = block_sum<NT>(ssq, red);
+  if (threadIdx.x == 0) s_inv = 1.0f / (sqrtf(0.f + sum) + eps);
+  __syncthreads();
+  const float inv = s_inv;
+  const int ts = opaque_lane((int)threadIdx.x);
 #pragma unroll
-    for (int k = 0; k < SV_VPT; ++k) {
-      const int v = k * NT + ts;
-      lds_u32x4* const px = reinterpret_cast<lds_u32x4*>(X + lds_pos(v / SV_VPR, v % SV_VPR, XCH));
-      *px = scale8(*px, inv);
-    }
-    __syncthreads();
-
-    ns_iterations<1, 4>(X, A, lane, steps, ca, cb, cc, round_once);
-
-    // ---- untile with WD/LR of this tile, gather of the next -----------------------
-    const int64_t nx = tt + gridDim.x;
-    if (nx < ntiles) {
-      ssq = step_io<DT, PDT, true, true>(params, n_params, X, tile_begin + tt, tile_begin + nx, tile_h, tile_w,
-                                         sa);
-      tt = nx;
-    } else {
-      step_io<DT, PDT, true, false>(params, n_params, X, tile_begin + tt, 0, tile_h, tile_w, sa);
-      break;
-    }
+  for (int k = 0; k < SV_VPT; ++k) {
+    const int v = k * NT + ts;
+    lds_u32x4* const px = reinterpret_cast<lds_u32x4*>(X + lds_pos(v / SV_VPR, v % SV_VPR, XCH));
+    *px = scale8(*px, inv);
   }
+  __syncthreads();
+
+  ns_iterations<1, 4>(X, A, lane, steps, ca, cb, cc, round_once);
+
+  // ---- untile with WD/LR ----------------------------------------------------------
+  step_io<DT, PDT, true, false>(params, n_params, X, tile_begin + tt, 0, tile_h, tile_w, sa);
 }
 
 int num_cus() {
@@ -657,18 +651,22 @@ bool lds_step_supported(int tile_h, int tile_w, int dtype, int param_dtype) {
 void lds_step_run(const HimuonParamDesc* params, int n_params, int64_t tile_begin, int64_t cnt, int tile_h,
                   int tile_w, int dtype, int param_dtype, int steps, float a, float b, float c, float eps,
                   bool round_once, const float* sa, hipStream_t s) {
-  const int64_t wgs = std::min<int64_t>(cnt, (int64_t)3 * 4 * num_cus());
-  const dim3 grid((unsigned)wgs), block(NT);
+  // one workgroup per tile, in launches of at most 2^30 workgroups
   const int ro = round_once ? 1 : 0;
-#define HM_LDS_STEP(D, PD)                                                                                  \
-  hipLaunchKernelGGL((lds_step_kernel<D, PD>), grid, block, 0, s, params, n_params, tile_begin, cnt, tile_h, \
+  const dim3 block(NT);
+  for (int64_t off = 0; off < cnt; off += (int64_t)1 << 30) {
+    const int64_t n = std::min<int64_t>(cnt - off, (int64_t)1 << 30);
+    const dim3 grid((unsigned)n);
+#define HM_LDS_STEP(D, PD)                                                                                    \
+  hipLaunchKernelGGL((lds_step_kernel<D, PD>), grid, block, 0, s, params, n_params, tile_begin + off, n, tile_h, \
                      tile_w, steps, a, b, c, eps, ro, sa)
-  if (dtype == HIMUON_DTYPE_F32) {
-    if (param_dtype == HIMUON_DTYPE_F32) HM_LDS_STEP(HIMUON_DTYPE_F32, HIMUON_DTYPE_F32);
-    else HM_LDS_STEP(HIMUON_DTYPE_F32, HIMUON_DTYPE_BF16);
-  } else {
-    if (param_dtype == HIMUON_DTYPE_F32) HM_LDS_STEP(HIMUON_DTYPE_BF16, HIMUON_DTYPE_F32);
-    else HM_LDS_STEP(HIMUON_DTYPE_BF16, HIMUON_DTYPE_BF16);
+    if (dtype == HIMUON_DTYPE_F32) {
+      if (param_dtype == HIMUON_DTYPE_F32) HM_LDS_STEP(HIMUON_DTYPE_F32, HIMUON_DTYPE_F32);
+      else HM_LDS_STEP(HIMUON_DTYPE_F32, HIMUON_DTYPE_BF16);
+    } else {
+      if (param_dtype == HIMUON_DTYPE_F32) HM_LDS_STEP(HIMUON_DTYPE_BF16, HIMUON_DTYPE_F32);
+      else HM_LDS_STEP(HIMUON_DTYPE_BF16, HIMUON_DTYPE_BF16);
+    }
   }
 #undef HM_LDS_STEP
 }
