@@ -460,7 +460,9 @@ __global__ __launch_bounds__(NTQ, NQ == 1 ? 3 : 1) void ns5_lds_kernel(const uin
 // 1 / (sqrt(s) + eps)).
 constexpr int SV_N = 128, SV_VPR = SV_N / 8;  // 16 vectors of 8 per NS row
 constexpr int SV_VPT = M * SV_VPR / NT;       // vectors per thread (8)
-constexpr int SV_BATCH = 2;                   // vectors loaded before any is used
+// vectors loaded before any is used: the untile all 8 (8 VGPRs each), the
+// gather 4 (16 VGPRs each; 8 would spill)
+constexpr int SV_BATCH_UNT = 8, SV_BATCH_GAT = 4;
 
 struct TileAt {
   const HimuonParamDesc* P;
@@ -503,6 +505,7 @@ HM_DEV float step_io(const HimuonParamDesc* __restrict__ params, int n_params, l
   // those iterations' registers)
   const int tq = opaque_lane((int)threadIdx.x);
   float ssq = 0.f;
+  constexpr int SV_BATCH = UNT ? SV_BATCH_UNT : SV_BATCH_GAT;
 #pragma unroll 1
   for (int b0 = 0; b0 < SV_VPT; b0 += SV_BATCH) {
     // phase 1: every global load of the batch (parameters of tile tu, or
