@@ -212,7 +212,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     const uint16_t* const nAt = g.A + ((more ? next : item) >> 2) * (int64_t)T * T;
     const int ni0 = P * (next & 3);
     float xs = 1.f;
-    if constexpr (SC) xs = g.xinv[tile];
+    if constexpr (SC) xs = uniform_load_f32(g.xinv, tile);
 
     // A_P landed: the ring loads of units 0..2 (and the stores between them)
     // were issued after its DMA.

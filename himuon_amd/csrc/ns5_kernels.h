@@ -58,6 +58,20 @@ HM_DEV u32x4_t scale8_rne(u32x4_t v, float s) {
   return o;
 }
 
+// p[i] for a wave-uniform p and i, read with a scalar load (written by an
+// earlier launch). The compiler makes a vector load of it in kernels that
+// also store to global memory, and the first use of that load then waits for
+// vmcnt(0): for every direct-to-LDS operand load in flight, which the
+// compiler does not count. The scalar load is waited for with lgkmcnt.
+HM_DEV float uniform_load_f32(const float* p, int64_t i) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)i);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)i >> 32));
+  const float* a = p + (int64_t)(((uint64_t)hi << 32) | lo);
+  float v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(a) : "memory");
+  return v;
+}
+
 // s_waitcnt with vmcnt = N (expcnt and lgkmcnt at their maxima) / lgkmcnt = N.
 template <int N>
 HM_DEV void wait_vm() {

@@ -39,6 +39,8 @@
 namespace {
 
 
+typedef __attribute__((address_space(3))) u32x4_t lds_u32x4;
+
 constexpr int BT = 256;               // output block edge
 constexpr int BK = 32;                // K per stream unit
 constexpr int SLOT = 32768;           // bytes per ring slot
@@ -201,7 +203,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   const int U = nk + NR;
   static_assert(!SC || MODE != kGramB, "GramB has no X operand");
   float xs = 1.f;
-  if constexpr (SC) xs = g.inv[tile];
+  if constexpr (SC) xs = uniform_load_f32(g.inv, tile);
 
   // ---- loaders ------------------------------------------------------------
   const ItemSrc src = item_src<MODE, NW>(g, it, lane, wave);
@@ -264,24 +266,38 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     }
   };
 
-  // X0 scaling of landed fragments (SC): GramA both operands, Apply the X one.
-  // Called right after the lgkmcnt wait for these fragments, before further
-  // LDS reads are issued. Apply's fragments come from inline-assembly reads
-  // that the compiler does not track, so each passes through a wait that
-  // names it as an operand: the scaling cannot be scheduled before the data
-  // has landed.
+  // X0 scaling (SC). Apply: the X fragments as they land, called right after
+  // the lgkmcnt wait for them, before further LDS reads are issued; they come
+  // from inline-assembly reads that the compiler does not track, so each
+  // passes through a wait that names it as an operand and the scaling cannot
+  // be scheduled before the data has landed.
   auto scale_frags = [&](u32x4_t(&fa)[TJ], u32x4_t(&fb)[4]) {
-    if constexpr (SC) {
-      if constexpr (kTr) {
+    (void)fb;
+    if constexpr (SC && kTr) {
 #pragma unroll
-        for (int t = 0; t < TJ; ++t) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[t]));
-      }
-      if constexpr (MODE == kGramA) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) fb[t] = scale8_rne(fb[t], xs);
-      }
+      for (int t = 0; t < TJ; ++t) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[t]));
 #pragma unroll
       for (int t = 0; t < TJ; ++t) fa[t] = scale8_rne(fa[t], xs);
+    }
+  };
+  // GramA: unit v in LDS, scaled in place once, each wave its own DMA'd
+  // 16-byte pieces (lane l's at 16 l of each of the wave's 1 KiB blocks),
+  // after its wait for them and before the barrier that publishes the unit:
+  // a third of the work of scaling every fragment read (each unit's bytes
+  // are read as fragments by three waves on average).
+  auto scale_unit = [&](int v) {
+    if constexpr (SC && MODE == kGramA) {
+      asm volatile("" ::: "memory");  // the reads below follow the vmcnt wait
+      lds_u8* const d = lds + (v % NSLOT) * SLOT + wave * 1024 + 16 * lane;
+#pragma unroll
+      for (int i = 0; i < 16 / NW; ++i) {
+        lds_u32x4* const p = reinterpret_cast<lds_u32x4*>(d + i * NW * 1024);
+        *p = scale8_rne(*p, xs);
+        if constexpr (!DIAG) {
+          lds_u32x4* const q = reinterpret_cast<lds_u32x4*>(d + HALF + i * NW * 1024);
+          *q = scale8_rne(*q, xs);
+        }
+      }
     }
   };
 
@@ -315,6 +331,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     for (int v = 0; v < DIST; ++v) issue(v);
   }
   wait_unit<L, NR, RL>(nk, 0, pre_st);
+  scale_unit(0);
   lds_barrier();  // unit 0 is in; every wave is past the previous epilogue's staging
   issue(DIST);
   u32x4_t fa0[TJ], fb0[4], fa1[TJ], fb1[4];
@@ -337,6 +354,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     wait_lgkm<0>();  // second-half fragments of unit u
     scale_frags(fa1, fb1);
     wait_unit<L, NR, RL>(nk, u + 1, pre_st);
+    scale_unit(u + 1);
     lds_barrier();
     mma_row(fa1, fb1, 0);
     __builtin_amdgcn_sched_barrier(0);
