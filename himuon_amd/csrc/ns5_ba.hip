@@ -10,45 +10,62 @@
 // (A = bf16(X X^T)) stays the streamed Gram kernel (ns5_stream.hip).
 //
 // Work item (tile t, panel p), rows i0 = 128 p .. i0 + 127, eight waves, two
-// per SIMD: wave w = 4 h + c owns output columns col0 = 128 c + 64 h ..
-// + 63 in both stages, as 2 x 4 v_mfma_f32_32x32x16_bf16 tiles (128 fp32
-// accumulators per lane), so that while one wave of a SIMD waits on a read
-// or works through an epilogue the other's MFMAs issue. Items are spread
-// persistently, a contiguous range per XCD.
+// per SIMD: wave w = 4 h + c (group h, SIMD c) owns output columns
+// col0 = 256 h + 64 c .. + 63 in both stages, as 2 x 4
+// v_mfma_f32_32x32x16_bf16 tiles (128 fp32 accumulators per lane). Items are
+// spread persistently, a contiguous range per XCD.
 //
 //  Stage 1: B_P[i][j] = bf16(c sum_k A[i0+i][k] A[j][k] + b A[i0+i][j]).
 //    Row-side operand A_P (128 x 512 bf16 = 128 KiB) resident in LDS region
-//    R, loaded with direct-to-LDS DMA during the previous item's stage 2, a
-//    quarter at a time as soon as every wave has read the B_P columns it
-//    replaces. Column-side operand: A is exactly symmetric, so A[j][k] =
-//    A[k][j] and the wave streams rows k of A restricted to its 64 columns.
+//    R. Column-side operand: A is exactly symmetric, so A[j][k] = A[k][j]
+//    and the wave streams rows k of A restricted to its 64 columns.
 //  Stage 2: X'_P[i][j] = bf16(bf16(sum_k B_P[i][k] X[k][j]) + a X[i0+i][j]).
 //    Row-side operand B_P, written over A_P in R by the stage-1 epilogue;
 //    column-side operand: rows k of X restricted to the wave's columns.
 //
-//  Both K loops run the same schedule: the streamed rows go from global
-//  memory into a four-unit register ring (a unit = 32 rows x 64 columns =
-//  two k-steps of 16, 4 x 16-byte loads per lane), three units ahead of the
-//  MFMAs; each k-step's 16 rows are written to one of two wave-private
-//  2 KiB staging buffers and read back as column fragments with
-//  ds_read_b64_tr_b16 (contraction along the rows). No workgroup barrier
-//  inside a loop: the staging buffers are private and a wave's LDS
-//  operations execute in order. After stage 2 the ring carries the X_P rows
-//  i0 .. i0 + 127 (the a X term).
+// Each wave runs six phases per item, each ended by a workgroup barrier:
+//   K1a, K1b  stage-1 K loop over k = 0..255, then k = 256..511
+//   E1        stage-1 epilogue: B_P = bf16(c acc + b A_P) over the wave's
+//             own 128 x 64 block column of A_P (block column 4 h + c)
+//   K2a, K2b  stage-2 K loop, the same two halves
+//   E2        stage-2 epilogue: + a X_P, stores of X'_P; direct-to-LDS load
+//             of the next item's A_P half h (block columns 4 h .. 4 h + 3)
+// Group 1 (waves 4..7) passes one extra barrier first, so it runs one phase
+// behind group 0 (waves 0..3): on every SIMD one wave's epilogue meets the
+// other wave's K loop, and the MFMA pipe has work while either epilogue runs.
+// Barrier segment s holds phase s of group 0 and phase s - 1 of group 1:
+//   K1a | E2(prev)    K1b | K1a    E1 | K1b    K2a | E1    K2b | K2a    E2 | K2b
+// which orders every LDS reuse of R:
+//  - E1 of group 0 (segment 3) overwrites A_P block columns 0..3, whose last
+//    readers are the K1a halves (segments 1, 2); E1 of group 1 (segment 4)
+//    block columns 4..7, last read in the K1b halves (segments 2, 3);
+//  - K2a (block columns 0..3 of B_P) starts after E1 of group 0, K2b (4..7)
+//    after E1 of group 1;
+//  - E2 of group 0 (segment 6) loads the next A_P's columns 0..3 after both
+//    K2a halves (segments 4, 5) and waits for them before its barrier, for
+//    the next K1a of group 0 (next segment 1); E2 of group 1 (next segment 1)
+//    loads columns 4..7 after both K2b halves (segments 5, 6), landed before
+//    the next K1b of group 0 (next segment 2).
+// Within a K-loop half the R fragments of the next k-step are read one k-step
+// ahead, but never across the half boundary (the other half of R may still be
+// written in that segment).
 //
-//  Stage-1 epilogue: B_P = bf16(c acc + b A_P) for the wave's own columns,
-//  read from and written to the same R addresses, between two barriers.
+//  K loops: the streamed rows go from global memory into a four-unit register
+//  ring (a unit = 32 rows x 64 columns = two k-steps of 16, 4 x 16-byte loads
+//  per lane), three units ahead of the MFMAs; each k-step's 16 rows are
+//  written to one of two wave-private 2 KiB staging buffers and read back as
+//  column fragments with ds_read_b64_tr_b16 (contraction along the rows).
+//  After stage 2 the ring carries the X_P rows i0 .. i0 + 127 (the a X term).
+//
 //  Stage-2 epilogue, per 32-row block: bf16(B X) through the wave's 4 KiB
 //  area into the row layout of the stores, + a X there with the X_P rows the
 //  ring holds in that layout, 128-byte row stores, and the next item's first
 //  ring units loaded. (The 2-D form rounds B X + a X once: X_P goes into the
 //  accumulator layout through the area instead, and the sum back.)
 //
-// Per item the waves meet at barriers: A_P landed, A_P reads done, B_P
-// written, a quarter of B_P read (three times inside stage 2), all of B_P
-// read. Each output element sums its k terms in one fp32 accumulator in
-// ascending k with the same MFMA as the three-kernel path, so results are
-// bit-identical to it.
+// Each output element sums its k terms in one fp32 accumulator in ascending k
+// with the same MFMA as the three-kernel path, so results are bit-identical
+// to it.
 //
 // LDS: R (128 KiB, 8-row blocks, below), then a 4 KiB area per wave: two
 // 2 KiB staging buffers (16 rows x 128 B, 16-byte chunk c of row r at
@@ -68,6 +85,7 @@ constexpr int WAREA = 4096;                 // per-wave staging
 constexpr int LDS_BYTES = R_BYTES + NW * WAREA;
 constexpr int NKS = T / 16;                 // k-steps per stage
 constexpr int NUNIT = T / 32;               // ring units per stage (2 k-steps each)
+constexpr int HUNIT = NUNIT / 2;            // ring units per K-loop half
 constexpr int NSLOT = 4;                    // ring slots
 constexpr int AHEAD = NSLOT - 1;            // units in flight ahead of the MFMAs
 static_assert(LDS_BYTES == 160 * 1024, "LDS budget");
@@ -113,6 +131,13 @@ struct Unit {
 // chunk) hit 16 distinct 16-byte bank groups.
 HM_DEV int r_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+// VMEM instructions a stage-2 epilogue issues after its direct-to-LDS loads
+// (at its second 32-row block) when another item follows: 3 x 4 row stores
+// and 2 x 4 ring loads. The wait for those loads allows this many younger
+// ones outstanding (vmcnt retires in issue order).
+constexpr int E2_VMEM_AFTER_DMA = 3 * 4 + (AHEAD - 1) * 4;
+static_assert(E2_VMEM_AFTER_DMA < 64, "vmcnt range");
+
 // SC (the first iteration): every X value (stage-2 rows, the a X term) is
 // replaced by bf16(x xinv[tile]) before it is used.
 template <bool ROUND_ONCE, bool SC>
@@ -121,7 +146,8 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
   lds_u8* const lds = (lds_u8*)lds_raw;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col0 = 128 * (wave & 3) + 64 * (wave >> 2);  // the wave's first output column
+  const int grp = wave >> 2, cw = wave & 3;
+  const int col0 = 256 * grp + 64 * cw;  // the wave's first output column
   const int l32 = lane & 31, hi = lane >> 5;
   const uint32_t r_base = (uint32_t)(uintptr_t)lds;
   // R row fragments: fragment (ti, ks) of lane l (row 32 ti + l32, chunk
@@ -149,7 +175,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
   // epilogue block (32 rows x 128 B, chunk c of row r at c ^ (r / 2) % 8)
   auto ep_off = [](int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); };
 
-  // (32-bit item indices: the launcher takes at most 2^29 tiles per call)
+  // (32-bit item indices: the launcher takes fewer than 2^29 tiles per call)
   const int total = (int)g.ntiles * (T / P);
   const int wper = (int)(gridDim.x >> 3);
   const int per_xcd = (total + 7) >> 3;
@@ -166,42 +192,46 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
 #pragma unroll
     for (int n = 0; n < 4; ++n) load_row(M, row0, d, n);
   };
-  // A_P into R, one block per instruction: lane l lands at row l / 8,
-  // position l % 8 and fetches chunk (l % 8) ^ swz(row). Call q (0..3) loads
-  // block columns m = 2 q, 2 q + 1 (k-steps 8 q .. 8 q + 7); wave w takes
-  // block rows g = 2 w, 2 w + 1 (ln, wv: the lane and wave index, opaque per
-  // call so the addresses are formed where they are used).
-  auto dma_ap = [&](const uint16_t* At, int i0, int q, int ln, int wv) {
+  // Half hh of A_P (block columns m = 4 hh .. 4 hh + 3, k = 256 hh ..) into
+  // R, one block per instruction: lane l lands at row l / 8, position l % 8
+  // and fetches chunk (l % 8) ^ swz(row); the wave of SIMD wv takes block
+  // rows 4 wv .. 4 wv + 3 (ln, wv: the lane and SIMD index, opaque per call
+  // so the addresses are formed where they are used). 16 instructions.
+  auto dma_half = [&](const uint16_t* At, int i0, int hh, int ln, int wv) {
 #pragma unroll
-    for (int gg = 0; gg < 2; ++gg) {
-      const int gb = 2 * wv + gg;
+    for (int gg = 0; gg < 4; ++gg) {
+      const int gb = 4 * wv + gg;
       const int rr = ln >> 3;
       const int ch = (ln & 7) ^ rr ^ (gg & 1);
-      const uint16_t* src = At + (i0 + 8 * gb + rr) * T + 128 * q + 8 * ch;
+      const uint16_t* src = At + (i0 + 8 * gb + rr) * T + 256 * hh + 8 * ch;
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) dma16(src + 64 * mm, r_base + 1024 * (8 * gb + 2 * q + mm));
+      for (int mm = 0; mm < 4; ++mm) dma16(src + 64 * mm, r_base + 1024 * (8 * gb + 4 * hh + mm));
     }
   };
 
   Unit ring[NSLOT];
   {
+    // the first item's whole A_P (each group its half) and stage-1 units
     const uint16_t* At = g.A + (item >> 2) * (int64_t)T * T;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) dma_ap(At, P * (int)(item & 3), q, lane, wave);
+    dma_half(At, P * (int)(item & 3), grp, lane, cw);
 #pragma unroll
     for (int u = 0; u < AHEAD; ++u) load_rows(At, 32 * u, ring[u]);
+    wait_vm<AHEAD * 4>();
+    lds_barrier();
   }
   const float ca = g.a, cb = g.b, cc = g.c;
+  // group 1 runs one phase behind group 0: its first segment is empty
+  if (grp == 1) lds_barrier();
 
   for (;;) {
     // The lane index, opaque per item: lane-dependent addresses are formed
     // inside the item loop, not hoisted out of it for the whole kernel (they
     // would not fit in the registers left beside the ring and accumulators).
     // (read by volatile assembly: a pure builtin would be hoisted and held.)
-    int lane_o, wave_o = wave;
+    int lane_o, cw_o = cw;
     uint32_t xl_o = x_lane;
     asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_o));
-    asm volatile("" : "+s"(wave_o), "+v"(xl_o));
+    asm volatile("" : "+s"(cw_o), "+v"(xl_o));
     const int64_t tile = item >> 2;
     const int i0 = P * (int)(item & 3);
     const uint16_t* At = g.A + tile * (int64_t)T * T;
@@ -214,11 +244,6 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     float xs = 1.f;
     if constexpr (SC) xs = uniform_load_f32(g.xinv, tile);
 
-    // A_P landed: the ring loads of units 0..2 (and the stores between them)
-    // were issued after its DMA.
-    wait_vm<3 * 4>();
-    lds_barrier();
-
     f32x16_t acc[2][4];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
@@ -227,14 +252,14 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
 
-    // ---- one K loop: acc += P_frag x (rows of M) over k = 0..511 ----------------------
+    // ---- one K-loop half: acc += P_frag x (rows of M), k = 256 hf .. + 255 ----------
     // k-step ks: its 16 rows (ring unit ks / 2, registers 2 (ks % 2) ..) go to
     // staging buffer ks % 2 and come back as column fragments through
     // transposing reads; the row fragments of the panel (A_P or B_P) come from
-    // R. After the first MFMA row of k-step ks, all of k-step ks + 1's reads;
-    // after the second, k-step ks + 2's rows into buffer ks % 2, behind those
-    // reads (a wave's LDS operations execute in order); after each row, one
-    // load of the unit three ahead.
+    // R. After the first MFMA row of k-step ks, all of k-step ks + 1's reads
+    // (within the half); after the second, k-step ks + 2's rows into buffer
+    // ks % 2, behind those reads (a wave's LDS operations execute in order);
+    // after each row, one load of the unit three ahead.
     u32x4_t fa[2][2], fb[2][4];
     auto read_frags = [&](int ks, int b) {
       const lds_u8* const rb = rfrag_base(ks);
@@ -263,13 +288,17 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
       M = v < NUNIT ? At : Xt;
       row0 = v < NUNIT ? 32 * v : v < 2 * NUNIT ? 32 * (v - NUNIT) : i0 + 32 * (v - 2 * NUNIT);
     };
-    auto kloop = [&](int base) {  // base: stream index of the stage's unit 0 (0 or 16)
+    // base: stream index of the stage's unit 0 (0 or 16); hf: the half
+    auto khalf = [&](int base, int hf) {
       const bool xrows = base == NUNIT;
-      write_rows(0, ring[base % NSLOT], xrows);
-      write_rows(1, ring[base % NSLOT], xrows);
-      read_frags(0, 0);
+      if (hf == 0) {
+        write_rows(0, ring[base % NSLOT], xrows);
+        write_rows(1, ring[base % NSLOT], xrows);
+      }
+      read_frags(2 * HUNIT * hf, 0);
 #pragma unroll
-      for (int u = 0; u < NUNIT; ++u) {
+      for (int uu = 0; uu < HUNIT; ++uu) {
+        const int u = HUNIT * hf + uu;
         const uint16_t* M;
         int row0;
         unit_src(base + u + AHEAD, M, row0);
@@ -281,7 +310,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
 #pragma unroll
           for (int ti = 0; ti < 4; ++ti) acc[0][ti] = mfma(fa[s][0], fb[s][ti], acc[0][ti]);
           __builtin_amdgcn_sched_barrier(0);
-          if (ks + 1 < NKS) read_frags(ks + 1, b);
+          if (ks + 1 < 2 * HUNIT * (hf + 1)) read_frags(ks + 1, b);
           load_row(M, row0, dst, 2 * s);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -297,27 +326,19 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
             load_row(Xt, i0 + 96, x3, 2 * s + 1);
           }
           __builtin_amdgcn_sched_barrier(0);
-          // Stage 2, after k-step 8 q + 7 (q < 3): every wave has consumed
-          // the B_P fragments of k-steps up to 8 q + 7 (block columns 2 q,
-          // 2 q + 1; the reads in flight are of k-step 8 q + 8), so after a
-          // barrier those blocks take the next item's A_P. The fourth quarter
-          // follows the loop.
-          if (xrows && (ks & 7) == 7 && ks + 1 < NKS && more) {
-            asm volatile("s_barrier" ::: "memory");
-            dma_ap(nAt, ni0, ks >> 3, lane_o, wave_o);
-            __builtin_amdgcn_sched_barrier(0);
-          }
         }
       }
     };
 
     // ---- stage 1: c A_P A^T -----------------------------------------------------------
-    kloop(0);
+    khalf(0, 0);
+    lds_barrier();
+    khalf(0, 1);
+    lds_barrier();
 
     // ---- stage-1 epilogue: B_P = bf16(c acc + b A_P) over A_P, own columns ----------
     // element (i = 32 ti + l32, j = col0 + 32 tj + 8 q + 4 hi + e): block
     // (4 ti + l32 / 8, col0 / 64), row l32 % 8, chunk 4 tj + q, bytes 8 hi ..
-    lds_barrier();  // every wave is done reading A_P fragments
     {
       const int el = lane_o & 31, esw = r_swz(el);
       lds_u8* const ep1 = lds + 8192 * (el >> 3) + 1024 * (col0 >> 6) + 128 * (el & 7) + 8 * (lane_o >> 5);
@@ -344,7 +365,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
           }
       }
     }
-    lds_barrier();  // B_P complete
+    lds_barrier();
 
 #pragma unroll
     for (int a = 0; a < 2; ++a)
@@ -354,14 +375,10 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
         for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
 
     // ---- stage 2: B_P X ---------------------------------------------------------------
-    kloop(NUNIT);
-    // All X_P units in before the last quarter of the next A_P's DMA is
-    // issued: a wait for an X_P unit after it would also wait for the DMA
-    // (vmcnt retires in order).
-    wait_vm<0>();
-    lds_barrier();  // every wave is done reading B_P: R is free
-    const int nitem = next;
-    if (more) dma_ap(nAt, ni0, 3, lane_o, wave_o);
+    khalf(NUNIT, 0);
+    lds_barrier();
+    khalf(NUNIT, 1);
+    lds_barrier();
 
     // ---- stage-2 epilogue -------------------------------------------------------------
     // X_P unit q (rows 32 q ..) sits in ring[(2 NUNIT + q) % NSLOT] = ring[q],
@@ -369,6 +386,16 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     const int el32 = lane_o & 31, ehi = lane_o >> 5, erow = lane_o >> 3, ech = lane_o & 7;
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
+      if (ti == 1 && more) {
+        // The next item's A_P half grp into R (its last readers, the K2
+        // halves of both groups over these block columns, are behind
+        // barriers). Every X_P unit is waited for first (only block 0's 4
+        // stores and 4 ring loads may stay in flight), with the compiler's
+        // own wait count, so that no wait for an X_P unit follows these
+        // loads: it would also wait for them (vmcnt retires in order).
+        wait_vm<8>();
+        dma_half(nAt, ni0, grp, lane_o, cw_o);
+      }
       const Unit& xp = ring[(2 * NUNIT + ti) % NSLOT];
       u32x4_t rows[4];
       if constexpr (!ROUND_ONCE) {
@@ -431,8 +458,14 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
       if (more && ti < AHEAD) load_rows(nAt, 32 * ti, ring[ti]);
     }
     if (!more) break;
-    item = nitem;
+    // this group's half of the next A_P landed (issued before the
+    // E2_VMEM_AFTER_DMA stores and loads above)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(E2_VMEM_AFTER_DMA) : "memory");
+    lds_barrier();
+    item = next;
   }
+  // group 0 passes one extra barrier, meeting group 1's last segment
+  if (grp == 0) lds_barrier();
 }
 
 int num_cus() {
