@@ -11,7 +11,6 @@ from __future__ import annotations
 
 import ctypes
 import math
-import os
 from ctypes import c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
@@ -162,7 +161,7 @@ _lib = None
 
 
 def lib_path() -> Path:
-    return Path(os.environ.get("HIMUON_LIB", str(LIB_PATH)))
+    return LIB_PATH
 
 
 def load() -> ctypes.CDLL:
@@ -239,25 +238,21 @@ def ns5_workspace_bytes(sub_batch: int, mp: int, np_: int) -> int:
 
 
 # himuon_ns5_ex flags (include/himuon_hip.h). Kernel families: AUTO picks per
-# geometry; BLOCK128 runs the 128x128-block kernels everywhere (comparison
-# runs). ROUND_ONCE: the reference's 2-D third product, bf16(B X + a X).
+# geometry (what the optimizer runs); BLOCK128 runs the 128x128-block kernels
+# everywhere and STREAM3 the three streamed products where AUTO fuses two
+# (comparison runs, named explicitly by the caller). ROUND_ONCE: the
+# reference's 2-D third product, bf16(B X + a X).
 NS_FAMILY_AUTO = 0
 NS_FAMILY_BLOCK128 = 1
 NS_FAMILY_STREAM3 = 2
 NS_ROUND_ONCE = 0x10
 NS_FAMILIES = {"auto": NS_FAMILY_AUTO, "block128": NS_FAMILY_BLOCK128, "stream3": NS_FAMILY_STREAM3}
-# Family every ns5() call runs unless it names one: "auto". Tests and
-# benchmarks that compare families set this attribute; the optimizer never does.
-ns_family_override = "auto"
 
 
 def default_sub_batch(n_tiles: int, mp: int, np_: int) -> int:
     """Tiles per NS sub-batch (one set of launches): about 2 GiB of bf16 NS
     operand (4096 tiles of 512x512), so each launch has >10k 256x256 blocks
     and launch tails stay small; the A/B workspace is twice that."""
-    env = os.environ.get("HIMUON_NS_SUB_BATCH")
-    if env:
-        return max(1, min(n_tiles, int(env)))
     target = 2 << 30
     return max(1, min(n_tiles, target // (mp * np_ * 2)))
 
@@ -301,16 +296,15 @@ def tile_scale(partials, per_tile, n_tiles, inv, eps=NS_EPS):
     )
 
 
-def ns5(x, y, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, NS_B, NS_C), family=None,
+def ns5(x, y, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, NS_B, NS_C), family="auto",
         round_once=False):
     """NS5 on tiles x; X ping-pongs into y: the result is in x for an even
-    step count and in y for an odd one. ``family`` (a key of NS_FAMILIES)
-    defaults to ``ns_family_override``; ``round_once`` selects the 2-D
-    rounding of the third product."""
+    step count and in y for an odd one. ``family``: a key of NS_FAMILIES;
+    ``round_once`` selects the 2-D rounding of the third product."""
     a, b, c = coeffs
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    flags = NS_FAMILIES[family or ns_family_override] | (NS_ROUND_ONCE if round_once else 0)
+    flags = _stage_flags(family, round_once)
     _check(
         load().himuon_ns5_ex(
             x.data_ptr(), y.data_ptr(), inv.data_ptr(), n_tiles, mp, np_, steps, a, b, c,
@@ -320,21 +314,21 @@ def ns5(x, y, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, 
     )
 
 
-def _stage_flags(family, round_once=False) -> int:
-    return NS_FAMILIES[family or ns_family_override] | (NS_ROUND_ONCE if round_once else 0)
+def _stage_flags(family="auto", round_once=False) -> int:
+    return NS_FAMILIES[family] | (NS_ROUND_ONCE if round_once else 0)
 
 
-def xxt(x, out, batch, M, K, family=None):
+def xxt(x, out, batch, M, K, family="auto"):
     _check(load().himuon_xxt(x.data_ptr(), out.data_ptr(), batch, M, K, _stage_flags(family), _stream()),
            "himuon_xxt")
 
 
-def ba_plus_caa(a, out, batch, M, alpha, beta, family=None):
+def ba_plus_caa(a, out, batch, M, alpha, beta, family="auto"):
     _check(load().himuon_ba_plus_caa(a.data_ptr(), out.data_ptr(), batch, M, alpha, beta, _stage_flags(family),
                                      _stream()), "himuon_ba_plus_caa")
 
 
-def bmm_add(b, x, out, batch, M, N, a, round_once=False, family=None):
+def bmm_add(b, x, out, batch, M, N, a, round_once=False, family="auto"):
     _check(load().himuon_bmm_add(b.data_ptr(), x.data_ptr(), out.data_ptr(), batch, M, N, a,
                                  _stage_flags(family, round_once), _stream()), "himuon_bmm_add")
 
@@ -348,9 +342,9 @@ def ba_bmm_add(a, x, out, batch, alpha, beta, gamma, round_once=False):
 
 def lds_step_supported(tile_h: int, tile_w: int, dtype, param_dtype) -> bool:
     """Buckets himuon_lds_step takes: 128 x 128 NS tiles without transpose,
-    fp32/bf16 grads and parameters, unless the 128-block family is forced."""
+    fp32/bf16 grads and parameters."""
     return (0 < tile_h <= tile_w <= 128 and dtype in (torch.float32, torch.bfloat16)
-            and param_dtype in (torch.float32, torch.bfloat16) and ns_family_override != "block128")
+            and param_dtype in (torch.float32, torch.bfloat16))
 
 
 def lds_step(desc_table, n_params, tile_begin, n_tiles, tile_h, tile_w, dtype, param_dtype, steps, scale_alpha,

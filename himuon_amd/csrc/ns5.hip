@@ -339,7 +339,9 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
     if (lds) {
       ns5_lds_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, s);
     } else if (st) {
-      ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, ba, wsA, wsB, s);
+      const int rc = ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, ba, wsA,
+                                    wsB, s);
+      if (rc) return rc;
     } else {
       const uint16_t* cur = x + o;
       uint16_t* nxt = y + o;
@@ -522,8 +524,8 @@ extern "C" int himuon_ba_bmm_add(const uint16_t* a, const uint16_t* x, uint16_t*
       (flags & ~HIMUON_NS_ROUND_ONCE))
     return HIMUON_EINVAL;
   if (batch == 0) return 0;
-  if (batch > (int64_t(1) << 29)) return HIMUON_EINVAL;  // 32-bit work-item indices
-  ns5_ba_run(a, x, out, nullptr, batch, gamma, beta, alpha, (flags & HIMUON_NS_ROUND_ONCE) != 0,
-             static_cast<hipStream_t>(stream));
+  if (!ns5_ba_run(a, x, out, nullptr, batch, gamma, beta, alpha, (flags & HIMUON_NS_ROUND_ONCE) != 0,
+                  static_cast<hipStream_t>(stream)))
+    return HIMUON_EINVAL;  // batch above kBaMaxTiles (32-bit work-item indices)
   return (int)hipGetLastError();
 }

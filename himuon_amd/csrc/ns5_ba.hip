@@ -175,7 +175,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
   // epilogue block (32 rows x 128 B, chunk c of row r at c ^ (r / 2) % 8)
   auto ep_off = [](int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); };
 
-  // (32-bit item indices: the launcher takes fewer than 2^29 tiles per call)
+  // (32-bit item indices: the launcher takes at most kBaMaxTiles tiles per call)
   const int total = (int)g.ntiles * (T / P);
   const int wper = (int)(gridDim.x >> 3);
   const int per_xcd = (total + 7) >> 3;
@@ -480,8 +480,10 @@ int num_cus() {
 
 bool ns5_ba_supported(int mp, int np) { return mp == T && np == T; }
 
-void ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, const float* xinv, int64_t cnt, float a,
+bool ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, const float* xinv, int64_t cnt, float a,
                 float b, float c, bool round_once, hipStream_t s) {
+  static_assert(kBaMaxTiles * (T / P) < (int64_t(1) << 31), "32-bit work-item indices");
+  if (cnt < 1 || cnt > kBaMaxTiles) return false;
   const int64_t items = cnt * (T / P);
   const int64_t per_xcd = (items + 7) / 8;
   const int64_t wgs_per_xcd = std::max<int64_t>(1, std::min<int64_t>(num_cus() / 8, per_xcd));
@@ -495,4 +497,5 @@ void ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, const float* 
     hipLaunchKernelGGL((ns_ba_kernel<false, true>), grid, dim3(NTH), 0, s, args);
   else
     hipLaunchKernelGGL((ns_ba_kernel<false, false>), grid, dim3(NTH), 0, s, args);
+  return true;
 }

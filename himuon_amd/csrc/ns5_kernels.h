@@ -156,18 +156,22 @@ HM_DEV u32x2_t quad_transpose(u32x2_t w, int k) {
 // between x and y. round_once: the third product
 // rounds bf16(B X + a X) once (the 2-D form) instead of bf16(bf16(B X) + a X).
 // fused_ba: the second and third products run as one kernel (ns5_ba.hip;
-// mp == np == 512), wsB unused.
+// mp == np == 512), wsB unused. Returns 0, or HIMUON_EINVAL (nothing
+// launched) when cnt is too large for the fused kernel.
 bool ns5_stream_supported(int mp, int np);
-void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
+int ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
                     float a, float b, float c, bool round_once, bool fused_ba, uint16_t* wsA, uint16_t* wsB,
                     hipStream_t s);
 
 // Fused B = bf16(c A A^T + b A), Y = bf16(bf16(B X) + a X) (ns5_ba.hip) on
 // `cnt` 512 x 512 tiles: A from the first product, X -> Y (Y != X). xinv
 // non-null: X is the raw tile and X0 = bf16(X xinv[tile]) is used in its
-// place (the first iteration).
+// place (the first iteration). Its work items are (tile, 128-row panel)
+// with 32-bit indices: cnt must lie in 1 .. kBaMaxTiles, else nothing is
+// launched and false returned.
+constexpr int64_t kBaMaxTiles = (int64_t(1) << 29) - 1;
 bool ns5_ba_supported(int mp, int np);
-void ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, const float* xinv, int64_t cnt, float a,
+bool ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, const float* xinv, int64_t cnt, float a,
                 float b, float c, bool round_once, hipStream_t s);
 
 // One NS product over `ntiles` batch entries on the 256-block stream kernels

@@ -603,9 +603,10 @@ void ns_stream_product(int mode, const uint16_t* P, int64_t p_bs, int ldp, const
 // One sub-batch of `cnt` tiles, `steps` >= 1 iterations, ping-ponging X
 // between x and y; the first iteration's kernels scale the raw x on load
 // (X0 is never written); A and B live in the workspace.
-void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
-                    float a, float b, float c, bool round_once, bool fused_ba, uint16_t* wsA, uint16_t* wsB,
-                    hipStream_t s) {
+int ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
+                   float a, float b, float c, bool round_once, bool fused_ba, uint16_t* wsA, uint16_t* wsB,
+                   hipStream_t s) {
+  if (fused_ba && cnt > kBaMaxTiles) return HIMUON_EINVAL;
   const int64_t sq = (int64_t)mp * mp, rect = (int64_t)mp * np;
   const int nb = mp / BT;
   const int64_t gram_items = cnt * (nb * (nb + 1) / 2);
@@ -620,7 +621,7 @@ void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int
     else
       launch<kGramA>(ga, gram_items, s);
     if (fused_ba) {  // B stays on chip: ns5_ba.hip
-      ns5_ba_run(wsA, cur, nxt, xinv, cnt, a, b, c, round_once, s);
+      if (!ns5_ba_run(wsA, cur, nxt, xinv, cnt, a, b, c, round_once, s)) return HIMUON_EINVAL;
       std::swap(cur, nxt);
       continue;
     }
@@ -634,4 +635,5 @@ void ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int
       launch<kApply>(ap, apply_items, s);
     std::swap(cur, nxt);
   }
+  return 0;
 }

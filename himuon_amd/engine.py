@@ -52,8 +52,14 @@ class TileGroup:
         upd_dtype: torch.dtype | None = None,
         apply_groups: list[int] | None = None,
         round_once: bool = False,
+        ns_family: str = "auto",
     ):
         self.tile_h, self.tile_w = int(tile_h), int(tile_w)
+        # NS kernel family (a key of _native.NS_FAMILIES): "auto" is the
+        # per-geometry choice the optimizer runs; the others are comparison runs.
+        if ns_family not in nat.NS_FAMILIES:
+            raise ValueError(f"unknown NS kernel family {ns_family!r}")
+        self.ns_family = ns_family
         # NS third product rounded once (the reference's 2-D addmm form,
         # himuon.py:249-253): full-matrix groups and 2-D newton_schulz calls.
         self.round_once = bool(round_once)
@@ -90,6 +96,7 @@ class TileGroup:
         self.updates = [] if self.fused else [torch.empty(g.shape, device=device, dtype=self.upd_dtype) for g in grads]
         self.upd_scales = list(upd_scales)
         self._sig = None
+        self._bound = None
         self.desc = None
         self.bind(grads, moms, mus, nesterovs)
 
@@ -131,8 +138,11 @@ class TileGroup:
             raise ValueError(f"{what} must be row-major (stride(1) == 1), got strides {t.stride()}")
 
     def bind(self, grads, moms, mus, nesterovs) -> bool:
-        """(Re)build the device descriptor table if any pointer or momentum
-        setting changed. Returns True if a new table was uploaded."""
+        """Rewrite the device descriptor table if any pointer or momentum
+        setting changed (in place: the table keeps its device address, so a
+        captured graph that reads it sees the new pointers). Returns True if
+        the table was written. The table holds raw pointers, so the group keeps
+        the bound grads and momentum buffers alive until release()."""
         sig = tuple(
             (g.data_ptr(), None if m is None else m.data_ptr(), float(mu), bool(nv))
             for g, m, mu, nv in zip(grads, moms, mus, nesterovs)
@@ -164,11 +174,24 @@ class TileGroup:
             d.nesterov = 1 if nesterovs[i] else 0
             d.group = self.apply_groups[i] if self.fused else 0
             descs.append(d)
-        self.desc = nat.make_desc_table(descs, self.device)
+        table = nat.make_desc_table(descs, self.device)
+        if self.desc is not None and self.desc.numel() == table.numel():
+            self.desc.copy_(table)
+        else:
+            self.desc = table
         self._sig = sig
-        # the table holds raw pointers: keep what they point at alive
         self._bound = (list(grads), list(moms))
         return True
+
+    def release(self) -> None:
+        """Drop the references bind() took, once every launch that reads the
+        bound tensors is enqueued and their owner keeps them (the optimizer's
+        parameters hold their grads, its state the momentum buffers). Memory
+        torch frees afterwards is reused only in stream order, after those
+        launches. Without this, an eager loop with zero_grad(set_to_none=True)
+        would keep the previous step's grads alive while backward allocates
+        the next ones."""
+        self._bound = None
 
     # -- launches ----------------------------------------------------------
     def gather(self) -> None:
@@ -189,14 +212,15 @@ class TileGroup:
         nat.ns5(
             r(self.tiles, start, count), r(self.alt, start, count),
             self.inv[start : start + count], count, self.mp, self.np, steps,
-            workspace, sub_batch, round_once=self.round_once,
+            workspace, sub_batch, family=self.ns_family, round_once=self.round_once,
         )
 
     def lds_step_ok(self) -> bool:
         """True when the whole step of this group runs as one launch per chunk
         (himuon_lds_step): fused mode, 128 x 128 NS tiles without transpose,
         fp32/bf16 grads and parameters."""
-        return self.fused and nat.lds_step_supported(self.tile_h, self.tile_w, self.dtype, self.upd_dtype)
+        return (self.fused and self.ns_family != "block128"
+                and nat.lds_step_supported(self.tile_h, self.tile_w, self.dtype, self.upd_dtype))
 
     def lds_step(self, start: int, count: int, steps: int, scale_alpha: torch.Tensor) -> None:
         """Momentum, gather, normaliser, NS and the untile with the WD/LR of
@@ -316,37 +340,61 @@ class AdamwTables:
             nat.adamw_step(table, n, n_chunks, dt, beta1s, beta2s, epss, bias)
 
 
-def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
+class _NsPlan:
+    """Device state of ``newton_schulz`` for one (batch shape, dtype, device,
+    rounding form, kernel family): a tile group over its own input and output
+    buffers, the sub-batch and the NS workspace, built once. A call copies the
+    input into ``xin`` and the result out of ``out``, so it neither allocates
+    device state (beyond the returned tensor) nor rewrites the descriptor
+    table, and repeated calls cost only the launches."""
+
+    def __init__(self, n: int, M: int, N: int, dtype: torch.dtype, device, round_once: bool, family: str):
+        self.xin = torch.empty((n * M, N), device=device, dtype=dtype)
+        self.grp = TileGroup(
+            params=[self.xin], grads=[self.xin], moms=[None], tile_h=M, tile_w=N, upd_scales=[1.0],
+            mus=[0.0], nesterovs=[False], device=device, dtype=dtype, round_once=round_once, ns_family=family,
+        )
+        self.out = self.grp.updates[0]
+        self.sub_batch = self.grp.default_sub_batch()
+        self.ws = torch.empty(max(1, self.grp.workspace_bytes(self.sub_batch)), device=device, dtype=torch.uint8)
+
+    def run(self, steps: int) -> torch.Tensor:
+        g = self.grp
+        g.gather()
+        g.ns(0, g.n_tiles, steps, self.ws, self.sub_batch)
+        g.untile(steps)
+        return self.out
+
+
+_NS_PLANS: "dict[tuple, _NsPlan]" = {}
+_NS_PLANS_MAX = 8
+
+
+def newton_schulz(G: torch.Tensor, steps: int = 5, family: str = "auto") -> torch.Tensor:
     """Batched NS5 of ``G`` (..., M, N) on the HIP path; same shape and dtype.
 
     The batch is viewed as one (B*M, N) matrix cut into M x N tiles, so the
     gather/untile kernels handle the cast, the transpose-if-tall and the
     padding (himuon.py:263-284, test_kernels.py:176-198). A 2-D ``G`` takes
     the reference's 2-D rounding of the third product (torch.addmm,
-    himuon.py:249-253); a batched one that of fused_bmm_add."""
+    himuon.py:249-253); a batched one that of fused_bmm_add. The device state
+    for a shape is built on its first call and reused (at most _NS_PLANS_MAX
+    shapes are kept, the oldest dropped first); the result is a new tensor.
+    ``family``: the NS kernel family (comparison runs; "auto" otherwise)."""
     assert G.ndim >= 2
     if not G.is_cuda:
         raise RuntimeError("HiMuon.newton_schulz runs on the HIP device only (no CPU path)")
     M, N = G.shape[-2], G.shape[-1]
     dtype = G.dtype if G.dtype in nat.DTYPE_CODES else torch.float32
-    flat = G.reshape(-1, M, N).to(dtype).contiguous().view(-1, N)
-    grp = TileGroup(
-        params=[flat],
-        grads=[flat],
-        moms=[None],
-        tile_h=M,
-        tile_w=N,
-        upd_scales=[1.0],
-        mus=[0.0],
-        nesterovs=[False],
-        device=G.device,
-        dtype=dtype,
-        round_once=G.ndim == 2,
-    )
-    out = grp.updates[0]
-    sb = grp.default_sub_batch()
-    ws = torch.empty(max(1, grp.workspace_bytes(sb)), device=G.device, dtype=torch.uint8)
-    grp.gather()
-    grp.ns(0, grp.n_tiles, steps, ws, sb)
-    grp.untile(steps)
-    return out.view(G.shape).to(G.dtype)
+    n = G.numel() // (M * N) if M * N else 0
+    if n == 0:
+        return torch.empty_like(G)
+    key = (n, M, N, dtype, G.device, G.ndim == 2, family)
+    plan = _NS_PLANS.pop(key, None)
+    if plan is None:
+        if len(_NS_PLANS) >= _NS_PLANS_MAX:
+            _NS_PLANS.pop(next(iter(_NS_PLANS)))
+        plan = _NsPlan(n, M, N, dtype, G.device, G.ndim == 2, family)
+    _NS_PLANS[key] = plan  # most recently used last
+    plan.xin.view(G.shape).copy_(G)
+    return plan.run(steps).view(G.shape).to(G.dtype, copy=True)

@@ -69,6 +69,10 @@ class HiMuon(Optimizer):
     # WD/LR) as one LDS-resident launch per chunk (himuon_lds_step); False
     # keeps the gather / NS / untile launches (same results, bit for bit).
     _fuse_lds_step: bool = True
+    # NS kernel family of every tile group (a key of _native.NS_FAMILIES):
+    # "auto", the per-geometry choice; the others are comparison runs, which
+    # also keep 128 x 128 buckets off the one-launch LDS step for "block128".
+    _ns_family: str = "auto"
 
     def __init__(
         self,
@@ -128,9 +132,11 @@ class HiMuon(Optimizer):
         # Device state of the HIP path, rebuilt after reconfigure().
         self._groups: "list[dict] | None" = None  # tiled buckets + full-NS shape groups
         self._workspace: "torch.Tensor | None" = None
-        # (param, param storage, grad storage) of every parameter with a grad
-        # when the device state (plan, descriptor tables, graph) was built.
+        # (param, param storage) of every parameter with a grad when the
+        # device state (plan, tile groups, graph) was built, and where those
+        # grads lived when the graph was captured.
         self._state_sig: "tuple | None" = None
+        self._grad_sig: "tuple | None" = None
 
         if lr_adjust not in ("none", "tile"):
             raise ValueError(f"lr_adjust must be 'none' or 'tile', got {lr_adjust!r}")
@@ -173,10 +179,7 @@ class HiMuon(Optimizer):
         self._cached_plan = None
         self._groups = None
         self._workspace = None
-        self._cuda_graph = None
-        self._graph_step_count = 0
-        self._pending_updates.clear()
-        self._apply_tables = None
+        self._drop_graph()
         self._adamw_tables = None
         self._adamw_sig = None
 
@@ -184,30 +187,44 @@ class HiMuon(Optimizer):
         """The rank-local tensor of a DTensor (shares its storage), else t."""
         return t.to_local() if self._is_dtensor(t) else t
 
-    def _storage_sig(self) -> tuple:
-        """Which parameters have a grad, and where each such parameter's and
-        grad's storage lives (the local shard's, for DTensors). The plan, the
-        device descriptor tables and a captured graph all hold these pointers."""
-        return tuple(
-            (id(p), self._local(p).data_ptr(), self._local(p.grad).data_ptr())
-            for g in self.param_groups
-            for p in g["params"]
-            if p.grad is not None
+    def _storage_sig(self) -> tuple[tuple, tuple]:
+        """(which parameters have a grad and where each such parameter's
+        storage lives, where each of those grads lives), for the local shard of
+        DTensors. The plan and tile groups depend on the first; the descriptor
+        tables and a captured graph hold pointers of both."""
+        with_grad = [p for g in self.param_groups for p in g["params"] if p.grad is not None]
+        return (
+            tuple((id(p), self._local(p).data_ptr()) for p in with_grad),
+            tuple(self._local(p.grad).data_ptr() for p in with_grad),
         )
 
+    def _drop_graph(self) -> None:
+        """Forget the captured graph (the next steps warm up and recapture);
+        the plan, tile groups and buffers stay."""
+        self._cuda_graph = None
+        self._graph_step_count = 0
+        self._pending_updates.clear()
+        self._apply_tables = None
+
     def _check_storage(self) -> None:
-        """Drop the plan, device state and graph when the set of parameters
-        with grads, or the storage of any of them or of its grad, changed since
-        they were built (the next steps warm up and recapture, as after
-        reconfigure; momentum and AdamW state are kept). The reference scans
-        the full-matrix parameters every step and skips those without a grad
-        (himuon.py:846-858) and reads p.data at every update
-        (himuon.py:222-228, 343-348)."""
-        sig = self._storage_sig()
-        if sig != self._state_sig:
+        """When the set of parameters with grads or the storage of any of
+        them changed since the device state was built, drop the plan, device
+        state and graph (the next steps warm up and recapture, as after
+        reconfigure; momentum and AdamW state are kept). When only grads moved
+        (zero_grad(set_to_none=True) between steps), keep the plan and tile
+        groups: eager steps rewrite their descriptor tables in place (bind()),
+        and a captured graph, which recorded the old pointers, is dropped and
+        recaptured. The reference scans the full-matrix parameters every step
+        and skips those without a grad (himuon.py:846-858) and reads p.data at
+        every update (himuon.py:222-228, 343-348)."""
+        struct, grads = self._storage_sig()
+        if struct != self._state_sig:
             if self._state_sig is not None:
                 self._invalidate_plan_cache()
-            self._state_sig = sig
+            self._state_sig = struct
+        elif grads != self._grad_sig and self._cuda_graph is not None:
+            self._drop_graph()
+        self._grad_sig = grads
 
     def _scale_alpha(self) -> list[float]:
         """(1 - lr*wd, -lr) per param group: the two factors of p.mul_(1 - lr*wd);
@@ -540,9 +557,12 @@ class HiMuon(Optimizer):
                 dtype=dtype,
                 upd_dtype=update_dtype(params, dtype),
                 apply_groups=gidx if fusable(params, gidx, dtype) else None,
+                ns_family=self._ns_family,
             )
             if not (self._fuse_lds_step and grp.lds_step_ok()):
-                # (a bucket whose step runs in LDS has no NS tile buffer)
+                # A bucket whose step runs in LDS (himuon_lds_step: 128 x 128
+                # NS tiles) has no tile buffer at all, so it registers none:
+                # its tiles exist only in LDS, one workgroup at a time.
                 self._concat_buffers[bucket["bucket_key"]] = grp.tiles
             out.append(
                 {
@@ -576,6 +596,7 @@ class HiMuon(Optimizer):
                 # the reference calls newton_schulz on the 2-D momentum
                 # (himuon.py:861), whose third product is torch.addmm (249-253)
                 round_once=True,
+                ns_family=self._ns_family,
             )
             out.append(
                 {
@@ -651,6 +672,7 @@ class HiMuon(Optimizer):
                     dtype=gl.dtype,
                     upd_dtype=update_dtype(slices, gl.dtype),
                     apply_groups=[gi] * n if fuse else None,
+                    ns_family=self._ns_family,
                 )
                 out.append(
                     {
@@ -765,6 +787,11 @@ class HiMuon(Optimizer):
         graph replay."""
         groups = self._ensure_device_state()
         stats = self._run_groups(groups) if groups else {"ns_gpu_ms": 0.0, "ns_launches": 0, "total_B": 0}
+        for g in groups or ():
+            # the launches are enqueued; the parameters hold their grads and
+            # self.state the momentum buffers (a captured graph needs them in
+            # place anyway, which _check_storage enforces)
+            g["tiles"].release()
         self._step_adamw_groups()
         if groups and "bank" in groups[0]:
             # the FSDP path's stats (himuon.py:1013-1018): one NS launch per bank

@@ -207,7 +207,8 @@ int himuon_bmm_add(const uint16_t* b, const uint16_t* x, uint16_t* out,
  * counterpart: it equals ba_plus_cAA (ba_plus_cAA.py:90-120) followed by
  * fused_bmm_add (fused_bmm_add.py:98-135), bit for bit. A: (batch, 512, 512)
  * bf16, exactly symmetric (an XXT output); X, out: (batch, 512, 512) bf16;
- * M == N == 512, batch <= 2^29; `flags` takes only HIMUON_NS_ROUND_ONCE.
+ * M == N == 512, batch < 2^29 (32-bit work-item indices; larger batches
+ * return HIMUON_EINVAL); `flags` takes only HIMUON_NS_ROUND_ONCE.
  */
 int himuon_ba_bmm_add(const uint16_t* a, const uint16_t* x, uint16_t* out,
                       int64_t batch, int M, int N, float alpha, float beta,

@@ -165,7 +165,9 @@ def test_ns5_ex_and_stage_argument_errors(lib):
     assert lib.himuon_ba_bmm_add(8, 16, 24, 1, 512, 1024, 1.0, 1.0, 1.0, 0, z) == -22
     assert lib.himuon_ba_bmm_add(8, 16, 16, 1, 512, 512, 1.0, 1.0, 1.0, 0, z) == -22
     assert lib.himuon_ba_bmm_add(8, 16, 24, 1, 512, 512, 1.0, 1.0, 1.0, 1, z) == -22
+    # 32-bit work-item indices (4 per tile): 2^29 - 1 tiles at most
     assert lib.himuon_ba_bmm_add(8, 16, 24, (1 << 29) + 1, 512, 512, 1.0, 1.0, 1.0, 0, z) == -22
+    assert lib.himuon_ba_bmm_add(8, 16, 24, 1 << 29, 512, 512, 1.0, 1.0, 1.0, 0, z) == -22
     assert lib.himuon_ba_bmm_add(8, 16, 24, 0, 512, 512, 1.0, 1.0, 1.0, 0x10, z) == 0
     # the LDS-resident step: tile_h <= tile_w <= 128, fp32/bf16 grads and parameters,
     # a descriptor table and a (scale, alpha) table, round-once the only flag

@@ -253,3 +253,60 @@ def test_cfg5_llama3_8b_tile128_then_reconfigure_512():
     _run(opt, 1)
     _whole_momentum(opt, params, [6], 2 * N_STEPS)
     _check_group(opt, 0, sample, 2 * N_STEPS, before, label=f"{config} after reconfigure(512)")
+
+
+@pytest.mark.parametrize("cuda_graph", [False, True])
+def test_cfg1_single_matrix_step(cuda_graph):
+    """cfg1 end to end: one 1024 x 1024 fp32 weight, fp32 grads ~N(0, 1e-3^2)
+    from a seed (new values every step), Nesterov momentum 0.95, tile 256 (16
+    NS tiles), lr 1e-2, wd 0.1, five steps (graph mode: two eager warm-up
+    steps, the capture with its replay, two replays). After every step:
+    * the momentum buffer equals oracle.momentum bit for bit;
+    * the parameter equals the oracle's step from the GPU's previous parameter
+      (momentum, tiling, untiling, lr scale 0.2 sqrt(256) and WD/LR roundings)
+      around torch's same-dtype NS5 on the GPU, bit for bit;
+    * the update of every NS tile is within the numpy oracle's NS5 noise floor
+      (per-tile relative Frobenius max 2e-2, mean 1e-2);
+    * the parameter is within the reference's 1e-2 self-consistency tolerance
+      of the numpy oracle's own trajectory (test_himuon_self_consistency.py:18)."""
+    print(f"[cfg1] cuda_graph={cuda_graph}", flush=True)
+    layers, shapes, T, pdtype, _ = bench.CONFIGS["cfg1"]
+    assert (layers, shapes, T, pdtype) == (1, [(1024, 1024)], 256, torch.float32)
+    gen = torch.Generator().manual_seed(1)
+    p = torch.nn.Parameter((torch.randn(1024, 1024, generator=gen) * 0.02).to("cuda"))
+    opt = HiMuon([{"params": [p], "use_muon": True}], lr=LR, weight_decay=WD, momentum=MU, nesterov=True,
+                 tile_size=T, cuda_graph=cuda_graph, cuda_graph_warmup=2)
+    ts = opt.param_groups[0]["tile_size"]
+    p_np = p.detach().cpu().numpy()
+    buf = None
+
+    def torch_ns(x, steps):
+        return ns5_torch_staged(torch.from_numpy(x).to("cuda"), steps).float().cpu().numpy()
+
+    for k in range(5):
+        g = (torch.randn(1024, 1024, generator=gen) * 1e-3)
+        if p.grad is None:
+            p.grad = torch.empty_like(p)
+        p.grad.copy_(g.to("cuda"))
+        prev = p.detach().cpu().numpy()
+        opt.step()
+        torch.cuda.synchronize()
+        gn = g.numpy()
+        got = p.detach().cpu().numpy()
+        op = O.OracleParam(p=prev, g=gn, buf=buf, tile=ts, lr=LR, wd=WD)
+        exp_t, nb, _ = O.step_param(op, ns=torch_ns)
+        exp_o, _, _ = O.step_param(op)
+        assert np.array_equal(opt.state[p]["momentum_buffer"].cpu().numpy(), nb), k
+        assert np.array_equal(got, exp_t), (k, int((got != exp_t).sum()))
+        base = prev * np.float32(1 - LR * WD)
+        d_got, d_exp = got - base, exp_o - base
+        errs = np.array([np.linalg.norm(d_got[r:r + T, c:c + T] - d_exp[r:r + T, c:c + T])
+                         / np.linalg.norm(d_exp[r:r + T, c:c + T]) for r in range(0, 1024, T) for c in range(0, 1024, T)])
+        print(f"  step {k}: update vs numpy oracle per tile max {errs.max():.4f} mean {errs.mean():.4f}", flush=True)
+        assert errs.max() <= 2e-2 and errs.mean() <= 1e-2
+        op_o = O.OracleParam(p=p_np, g=gn, buf=buf, tile=ts, lr=LR, wd=WD)
+        p_np, _, _ = O.step_param(op_o)
+        np.testing.assert_allclose(got, p_np, rtol=1e-2, atol=1e-2)
+        buf = nb
+    if cuda_graph:
+        assert opt._cuda_graph is not None

@@ -70,13 +70,13 @@ GATHER_CASES = [
 
 
 @pytest.fixture(params=["auto", "stream3", "block128"])
-def ns_family(request, monkeypatch):
-    """Run a test under each NS kernel family selection: "auto" (the
-    product's per-geometry choice: LDS-resident, the fused GramB/Apply kernel
-    for 512 x 512 tiles, persistent streamed 256-blocks or 128-blocks),
-    "stream3" (the three streamed products where AUTO fuses two) and
-    "block128" (the 128-block kernels for every geometry)."""
-    monkeypatch.setattr(nat, "ns_family_override", request.param)
+def ns_family(request):
+    """Run a test under each NS kernel family selection, passed explicitly
+    to newton_schulz / TileGroup: "auto" (the product's per-geometry choice:
+    LDS-resident, the fused GramB/Apply kernel for 512 x 512 tiles, persistent
+    streamed 256-blocks or 128-blocks), "stream3" (the three streamed products
+    where AUTO fuses two) and "block128" (the 128-block kernels for every
+    geometry)."""
     return request.param
 
 
@@ -155,8 +155,8 @@ def test_untile_bit_exact(name, shapes, th, tw, dtype, nesterov):
 # ---------------------------------------------------------------------------
 # NS5
 # ---------------------------------------------------------------------------
-def _ns_engine(G: torch.Tensor, steps=5) -> torch.Tensor:
-    return newton_schulz(G, steps=steps)
+def _ns_engine(G: torch.Tensor, steps=5, family="auto") -> torch.Tensor:
+    return newton_schulz(G, steps=steps, family=family)
 
 
 NS_SHAPES = [
@@ -180,7 +180,7 @@ def test_newton_schulz_matches_reference_on_well_conditioned(label, shape, ns_fa
     north star's per-tile relative Frobenius bound (1e-2)."""
     print(f"[ns5 wc] {label} {shape} {ns_family}", flush=True)
     G = well_conditioned(shape, torch.bfloat16, seed=0)
-    out = _ns_engine(G)
+    out = _ns_engine(G, family=ns_family)
     assert out.shape == G.shape and out.dtype == G.dtype
     assert torch.isfinite(out).all()
     ref_eager = ns5_torch_eager(G)
@@ -200,7 +200,7 @@ def test_ns5_random_tiles_vs_oracle_and_torch(T, n, ns_family):
     references themselves (the summation-order noise floor of bf16 NS5)."""
     print(f"[ns5 random] T={T} n={n} {ns_family}", flush=True)
     G = _cpu_randn((n, T, T), seed=T, scale=1e-3).to(DEV)
-    out = _ns_engine(G)
+    out = _ns_engine(G, family=ns_family)
     ref_t = ns5_torch_staged(G)
     ref_o = torch.from_numpy(O.ns5_staged(G.cpu().numpy())).to(DEV)
     e_t = per_tile_rel_fro(out, ref_t)
@@ -221,7 +221,7 @@ def test_ns5_random_tiles_vs_oracle_and_torch(T, n, ns_family):
 @pytest.mark.parametrize("T,n", [(128, 16), (512, 4)])
 def test_ns5_singular_value_band(T, n, ns_family):
     G = _cpu_randn((n, T, T), seed=T + 1, scale=1e-3).to(DEV)
-    out = _ns_engine(G).double()
+    out = _ns_engine(G, family=ns_family).double()
     sv = torch.linalg.svdvals(out).cpu().numpy()
     ref_sv = torch.linalg.svdvals(ns5_torch_staged(G).double()).cpu().numpy()
     sv_in = torch.linalg.svdvals(G.double()).cpu().numpy()
@@ -243,10 +243,10 @@ def test_ns5_zero_tile_and_padding(ns_family):
     # the same block NS'd in its own 128x128 padding, bit for bit)
     G = torch.zeros(3, 256, 256, device=DEV)
     G[1, :37, :100] = _cpu_randn((37, 100), 4).to(DEV)
-    out = _ns_engine(G)
+    out = _ns_engine(G, family=ns_family)
     assert (out[0] == 0).all() and (out[2] == 0).all()
     assert (out[1, 37:] == 0).all() and (out[1, :, 100:] == 0).all()
-    small = _ns_engine(G[1:2, :37, :100].contiguous())
+    small = _ns_engine(G[1:2, :37, :100].contiguous(), family=ns_family)
     assert torch.equal(out[1, :37, :100], small[0])
 
 
@@ -257,7 +257,7 @@ def test_ns5_steps_honoured(steps, shape, ns_family):
     """Every step count, on the stream geometry and on the LDS-resident
     kernel's (which writes an even step count's result in place)."""
     G = _cpu_randn(shape, seed=9).to(DEV)
-    out = _ns_engine(G, steps=steps)
+    out = _ns_engine(G, steps=steps, family=ns_family)
     ref = torch.from_numpy(O.ns5_staged(G.cpu().numpy(), steps=steps)).to(DEV)
     assert per_tile_rel_fro(out, ref).max() <= 1.5e-2
     assert torch.equal(out, ns5_torch_staged(G, steps=steps).to(out.dtype))
@@ -267,7 +267,7 @@ def test_ns5_sub_batch_invariance(ns_family):
     """Sub-batching (tiles are independent) does not change results bitwise."""
     G = _cpu_randn((10, 256, 256), seed=12, scale=1e-3).to(DEV)
     grp = TileGroup([G.view(-1, 256)], [G.view(-1, 256)], [None], 256, 256, [1.0], [0.0], [False],
-                    torch.device(DEV), torch.float32)
+                    torch.device(DEV), torch.float32, ns_family=ns_family)
     outs = []
     for sb in (1, 3, 10):
         grp.gather()  # NS overwrites both X orientations (ping-pong): re-gather each run
@@ -301,7 +301,8 @@ def test_ns5_ignores_stale_buffer_contents(label, n, M, N, ns_family):
     outs = []
     for fill in (0.0, float("nan")):
         flat = G.reshape(-1, N)
-        grp = TileGroup([flat], [flat], [None], M, N, [1.0], [0.0], [False], torch.device(DEV), torch.bfloat16)
+        grp = TileGroup([flat], [flat], [None], M, N, [1.0], [0.0], [False], torch.device(DEV), torch.bfloat16,
+                        ns_family=ns_family)
         sb = grp.default_sub_batch()
         ws = torch.empty(max(2, grp.workspace_bytes(sb)), device=DEV, dtype=torch.uint8)
         grp.tiles.fill_(fill)

@@ -24,6 +24,8 @@ pytestmark = pytest.mark.gpu
 if torch.cuda.is_available():
     from himuon_amd.optimizers.himuon import HiMuon
 
+    from gpu_ref import ns5_torch_staged
+
 DEV = "cuda"
 RTOL = ATOL = 1e-2  # reference self-consistency tolerance (test_himuon_self_consistency.py:18)
 
@@ -88,6 +90,21 @@ def test_step_matches_oracle(name, shapes, tile, dtype):
                                p_dtype=dname, g_dtype=dname)
             p_np[i], bufs[i], _ = O.step_param(op)
             if dtype != torch.float32:
+                # bf16 parameters: this step from the GPU's own previous
+                # parameters and momentum, with the oracle's momentum, tiling,
+                # untiling, scale and WD/LR roundings around torch's
+                # same-dtype NS5 on the GPU, which the library's NS5 equals bit
+                # for bit: the new parameters must match bit for bit (the
+                # numpy NS5's summation order would move single bf16 roundings)
+                def torch_ns(x, steps):
+                    t = torch.from_numpy(x).to(DEV)
+                    return ns5_torch_staged(t, steps, round_once=x.ndim == 2).float().cpu().numpy()
+
+                op_gpu = O.OracleParam(p=prev[i], g=g_np[i], buf=None if k == 0 else bufs_prev[i], tile=ts,
+                                       lr=lr, wd=wd, p_dtype=dname, g_dtype=dname)
+                exp_p, _, _ = O.step_param(op_gpu, ns=torch_ns)
+                got = _np(p)
+                assert np.array_equal(got, exp_p), (name, i, k, int((got != exp_p).sum()), got.size)
                 continue
             # this step's update, per NS tile, from the GPU's own previous
             # parameters: relative Frobenius error at the noise floor of
@@ -531,3 +548,85 @@ def test_param_storage_change_is_followed(cuda_graph):
     torch.cuda.synchronize()
     assert torch.equal(old, old_copy), "the old parameter storage was written"
     assert not torch.equal(p.detach(), new_before), "the new parameter storage was not updated"
+
+
+@pytest.mark.parametrize("cuda_graph", [False, True])
+def test_fresh_grads_every_step_keep_the_device_state(cuda_graph):
+    """zero_grad(set_to_none=True) between steps (train.py --no-cuda-graph,
+    train_fsdp.py): every backward allocates new grads. The plan and tile
+    groups stay the same objects (only the descriptor tables are rewritten, in
+    place), no old grad is kept alive, and the parameters equal those of a run
+    whose grads are filled in place, bit for bit. In graph mode the moved
+    grads drop the captured graph (never replayed on stale pointers), which
+    is then warmed up and recaptured. The previous grads stay referenced here
+    until the new ones exist, so the new ones cannot reuse their memory."""
+    shapes = [(512, 1024), (256, 512), (1024, 512), (64, 64)]
+    m_a = make_model(shapes, torch.bfloat16, bias=True)
+    m_b = copy.deepcopy(m_a)
+    kw = dict(lr=0.02, weight_decay=0.1, tile_size=256, cuda_graph=cuda_graph, cuda_graph_warmup=2)
+    o_a = HiMuon(muon_groups(m_a, wd=0.1), **kw)
+    o_b = HiMuon(muon_groups(m_b, wd=0.1), **kw)
+    groups = None
+    for k in range(6):
+        seed_grads(m_a, 500 + k)
+        o_a.step()
+        old = [p.grad for p in m_b.parameters()]
+        for p in m_b.parameters():
+            p.grad = None  # zero_grad(set_to_none=True)
+        seed_grads(m_b, 500 + k)  # fresh grad tensors
+        if k >= 1:
+            assert all(p.grad.data_ptr() != o.data_ptr() for p, o in zip(m_b.parameters(), old))
+        del old
+        o_b.step()
+        if k >= 1:
+            assert o_b._groups is groups, "tile groups rebuilt for fresh grads"
+        groups = o_b._groups
+        for g in o_b._groups:
+            assert g["tiles"]._bound is None  # the step kept no grad alive
+        torch.cuda.synchronize()
+    for a, b in zip(m_a.parameters(), m_b.parameters()):
+        assert torch.equal(a, b)
+    if cuda_graph:
+        assert o_a._cuda_graph is not None  # in-place grads: captured and replayed
+
+
+def test_last_step_stats():
+    """_last_step_stats after an eager step: the NS launches (one per chunk),
+    the tiles they took (total_B = every bucket's B_total), the mean batch and
+    the eager NS time; zeros after a graph replay (himuon.py:812-825,
+    1103-1108)."""
+    model = make_model(MULTI)
+    opt = HiMuon(muon_groups(model), tile_size=256, b_hw=7, cuda_graph=True, cuda_graph_warmup=1)
+    seed_grads(model, 31)
+    opt.step()
+    st = opt._last_step_stats
+    plan = opt.xlayer_plan()
+    n_full = sum(1 for g in opt._groups if g["full"])
+    tiles_full = sum(g["tiles"].n_tiles for g in opt._groups if g["full"])
+    assert st["ns_launches"] == sum(b["n_calls"] for b in plan) + n_full
+    assert st["total_B"] == sum(b["B_total"] for b in plan) + tiles_full
+    assert st["avg_batch"] == pytest.approx(st["total_B"] / st["ns_launches"])
+    assert st["ns_gpu_ms"] > 0.0
+    for k in range(3):  # capture, then replays
+        seed_grads(model, 32 + k)
+        opt.step()
+    assert opt._cuda_graph is not None
+    assert opt._last_step_stats == {"ns_gpu_ms": 0.0, "ns_launches": 0, "total_B": 0, "avg_batch": 0.0}
+
+
+def test_lds_step_buckets_register_no_concat_buffer():
+    """A 128 x 128-tile bucket runs its whole step in LDS (himuon_lds_step):
+    it has no tile buffer, so _concat_buffers holds no entry for it; a 256
+    bucket of the same model holds its bf16 (n_tiles, 256, 256) buffer."""
+    model = make_model([(512, 1024), (256, 512)], torch.float32)
+    groups = [{"params": [model[0].weight], "use_muon": True, "tile_size": (128, 128)},
+              {"params": [model[1].weight], "use_muon": True, "tile_size": (256, 256)}]
+    opt = HiMuon(groups, cuda_graph=False)
+    seed_grads(model, 41)
+    opt.step()
+    keys = {b["bucket_key"] for b in opt.xlayer_plan()}
+    assert (128, 128, False, torch.float32) in keys and (256, 256, False, torch.float32) in keys
+    assert set(opt._concat_buffers) == {(256, 256, False, torch.float32)}
+    buf = opt._concat_buffers[(256, 256, False, torch.float32)]
+    assert buf.dtype == torch.bfloat16 and tuple(buf.shape) == (2, 256, 256)
+    assert any(g["tiles"].lds_step_ok() for g in opt._groups)
