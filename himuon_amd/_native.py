@@ -18,9 +18,11 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libhimuon_hip.so"
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 NS_ALIGN = 128
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+# Operand dtypes of the typed stage products (himuon_*_typed): the above and fp8 e5m2.
+PRODUCT_IN_CODES = {**DTYPE_CODES, **({torch.float8_e5m2: 3} if hasattr(torch, "float8_e5m2") else {})}
 
 # Quintic coefficients and normaliser epsilon (himuon.py:237,242; ns5_smem.py:26-30).
 NS_A, NS_B, NS_C = 3.4445, -4.7750, 2.0315
@@ -128,6 +130,11 @@ _SIGNATURES = {
     "himuon_bmm_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_int, c_void_p]),
     "himuon_ba_bmm_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_float, c_float,
                                   c_int, c_void_p]),
+    "himuon_xxt_typed": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p]),
+    "himuon_ba_plus_caa_typed": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_float, c_float, c_int, c_int,
+                                         c_void_p]),
+    "himuon_bmm_add_typed": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_int, c_int,
+                                     c_void_p]),
     "himuon_lds_step": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int, c_int, c_int, c_int, c_int, c_float,
                                 c_float, c_float, c_float, c_int, c_void_p, c_void_p]),
     "himuon_ns5_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_float, c_float,
@@ -331,6 +338,28 @@ def ba_plus_caa(a, out, batch, M, alpha, beta, family="auto"):
 def bmm_add(b, x, out, batch, M, N, a, round_once=False, family="auto"):
     _check(load().himuon_bmm_add(b.data_ptr(), x.data_ptr(), out.data_ptr(), batch, M, N, a,
                                  _stage_flags(family, round_once), _stream()), "himuon_bmm_add")
+
+
+def xxt_typed(x, out, batch, M, K):
+    """out = x x^T for any operand dtype of PRODUCT_IN_CODES, out fp32/bf16/fp16."""
+    _check(load().himuon_xxt_typed(x.data_ptr(), out.data_ptr(), batch, M, K, PRODUCT_IN_CODES[x.dtype],
+                                   DTYPE_CODES[out.dtype], _stream()), "himuon_xxt_typed")
+
+
+def ba_plus_caa_typed(a, out, batch, M, alpha, beta):
+    """out = alpha a a^T + beta a, any operand dtype of PRODUCT_IN_CODES."""
+    _check(load().himuon_ba_plus_caa_typed(a.data_ptr(), out.data_ptr(), batch, M, alpha, beta,
+                                           PRODUCT_IN_CODES[a.dtype], DTYPE_CODES[out.dtype], _stream()),
+           "himuon_ba_plus_caa_typed")
+
+
+def bmm_add_typed(b, x, out, batch, M, N, a):
+    """out = out_dtype(b x) + a x, any operand dtype of PRODUCT_IN_CODES."""
+    if b.dtype != x.dtype:
+        raise TypeError(f"bmm_add_typed: operands of one dtype expected, got {b.dtype} and {x.dtype}")
+    _check(load().himuon_bmm_add_typed(b.data_ptr(), x.data_ptr(), out.data_ptr(), batch, M, N, a,
+                                       PRODUCT_IN_CODES[x.dtype], DTYPE_CODES[out.dtype], _stream()),
+           "himuon_bmm_add_typed")
 
 
 def ba_bmm_add(a, x, out, batch, alpha, beta, gamma, round_once=False):

@@ -38,12 +38,15 @@
 extern "C" {
 #endif
 
-#define HIMUON_ABI_VERSION 3
+#define HIMUON_ABI_VERSION 4
 
 /* Element type codes for gradients / momentum / updates. */
 #define HIMUON_DTYPE_F32 0
 #define HIMUON_DTYPE_BF16 1
 #define HIMUON_DTYPE_F16 2
+/* fp8 e5m2 (OCP: 5 exponent bits, bias 15): operands of the typed stage
+ * products only (himuon_*_typed). */
+#define HIMUON_DTYPE_E5M2 3
 
 /* NS tile buffer dimensions (mp, np) must be multiples of this. */
 #define HIMUON_NS_ALIGN 128
@@ -196,6 +199,32 @@ int himuon_xxt(const uint16_t* x, uint16_t* out, int64_t batch, int M, int K,
                int flags, void* stream);
 int himuon_ba_plus_caa(const uint16_t* a, uint16_t* out, int64_t batch, int M,
                        float alpha, float beta, int flags, void* stream);
+/*
+ * The same three products for every operand dtype the reference's kernels
+ * take: tl.dot on the loaded dtype with an fp32 accumulator, the result cast to
+ * the dtype of `out` (XXT.py:62-63, ba_plus_cAA.py:65-85, fused_bmm_add.py:73-88;
+ * exercised with bf16, fp16, fp32 and fp8 e5m2 operands in
+ * tests/integration/test_kernels.py:36-165):
+ *   himuon_xxt_typed:         out = x x^T                  x: (batch, M, K)
+ *   himuon_ba_plus_caa_typed: out = alpha a a^T + beta a   a: (batch, M, M)
+ *   himuon_bmm_add_typed:     out = out_t(b x) + a x       b: (batch, M, M), x: (batch, M, N)
+ *                             (b x rounded to the output dtype before the add)
+ * in_dtype: HIMUON_DTYPE_F32, _BF16, _F16 or _E5M2 (every operand); out_dtype:
+ * HIMUON_DTYPE_F32, _BF16 or _F16. bf16 and fp16 operands run the MFMAs of their
+ * type, e5m2 ones the fp16 MFMA (exact widening), fp32 ones three bf16 MFMAs
+ * per product (16 significant bits of each operand). M, N multiples of
+ * HIMUON_NS_ALIGN, K a multiple of 64; contiguous batches; outputs must not
+ * alias inputs; at most 2^31 - 8 output blocks of 128 x 128 per call.
+ */
+int himuon_xxt_typed(const void* x, void* out, int64_t batch, int M, int K,
+                     int in_dtype, int out_dtype, void* stream);
+int himuon_ba_plus_caa_typed(const void* a, void* out, int64_t batch, int M,
+                             float alpha, float beta, int in_dtype,
+                             int out_dtype, void* stream);
+int himuon_bmm_add_typed(const void* b, const void* x, void* out,
+                         int64_t batch, int M, int N, float a, int in_dtype,
+                         int out_dtype, void* stream);
+
 int himuon_bmm_add(const uint16_t* b, const uint16_t* x, uint16_t* out,
                    int64_t batch, int M, int N, float a, int flags, void* stream);
 

@@ -169,6 +169,22 @@ def test_ns5_ex_and_stage_argument_errors(lib):
     assert lib.himuon_ba_bmm_add(8, 16, 24, (1 << 29) + 1, 512, 512, 1.0, 1.0, 1.0, 0, z) == -22
     assert lib.himuon_ba_bmm_add(8, 16, 24, 1 << 29, 512, 512, 1.0, 1.0, 1.0, 0, z) == -22
     assert lib.himuon_ba_bmm_add(8, 16, 24, 0, 512, 512, 1.0, 1.0, 1.0, 0x10, z) == 0
+    # the typed stage products: operand dtypes 0..3 (fp8 e5m2 = 3), output 0..2,
+    # M (and N) multiples of 128, K of 64, no aliasing, at most 2^31 - 8 blocks
+    assert lib.himuon_xxt_typed(8, 16, 0, 128, 64, 3, 2, z) == 0  # empty batch: no launch
+    assert lib.himuon_xxt_typed(8, 16, 1, 128, 64, 4, 2, z) == -22
+    assert lib.himuon_xxt_typed(8, 16, 1, 128, 64, 3, 3, z) == -22  # no fp8 output
+    assert lib.himuon_xxt_typed(8, 16, 1, 100, 64, 0, 0, z) == -22
+    assert lib.himuon_xxt_typed(8, 16, 1, 128, 96, 0, 0, z) == -22
+    assert lib.himuon_xxt_typed(8, 8, 1, 128, 64, 0, 0, z) == -22
+    assert lib.himuon_xxt_typed(8, 16, 1 << 31, 128, 64, 0, 0, z) == -22
+    assert lib.himuon_ba_plus_caa_typed(8, 16, 1, 200, 1.0, 1.0, 2, 2, z) == -22
+    assert lib.himuon_ba_plus_caa_typed(0, 16, 1, 128, 1.0, 1.0, 2, 2, z) == -22
+    assert lib.himuon_bmm_add_typed(8, 16, 16, 1, 128, 128, 1.0, 2, 2, z) == -22
+    assert lib.himuon_bmm_add_typed(8, 16, 24, 1, 128, 100, 1.0, 2, 2, z) == -22
+    assert lib.himuon_bmm_add_typed(8, 16, 24, 1, 128, 128, 1.0, 2, -1, z) == -22
+    assert lib.himuon_bmm_add_typed(8, 16, 24, 1 << 31, 128, 128, 1.0, 2, 2, z) == -22
+    assert lib.himuon_bmm_add_typed(8, 16, 24, 0, 128, 128, 1.0, 3, 0, z) == 0
     # the LDS-resident step: tile_h <= tile_w <= 128, fp32/bf16 grads and parameters,
     # a descriptor table and a (scale, alpha) table, round-once the only flag
     def lds(prm=8, npar=1, base=0, n=0, th=128, tw=128, dt=0, pdt=1, steps=5, flags=0x10, sa=16):
