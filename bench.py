@@ -46,19 +46,26 @@ NS_KERNELS = {
     "stream": "ns5 stage: ns_st_kernel<0> (X X^T), <1> (c A A^T + b A), <2> (B X + a X) per iteration",
     "lds": "ns5 stage: ns5_lds_kernel (all 5 iterations of a 128-row tile resident in LDS)",
     "small": "ns5 stage: ns_gram_kernel x2 + ns_apply_kernel per iteration",
+    "few_rows": "ns5 stage: ns5_small_kernel (all 5 iterations of a tile's 16, 32 or 64 rows resident in LDS)",
 }
 
 
-def ns_family(mp: int, np_: int, family: str = "auto") -> str:
+def ns_family(mp: int, np_: int, family: str = "auto", rows: int = 0) -> str:
     """The NS kernel family the library runs for an (mp, np) tile buffer
     (himuon_ns5_ex dispatch): with family "block128" the 128-blocks
     everywhere; with "stream3" the three streamed 256-block products wherever
-    both edges are multiples of 256; with "auto", LDS-resident for mp == 128
-    and np in {128, 256, 512}, the Gram kernel plus the fused GramB/Apply kernel for
-    512 x 512 tiles, streamed 256-blocks for other multiples of 256, else
-    128-blocks."""
+    both edges are multiples of 256; with "auto", the operand's own 16, 32 or
+    64 rows in LDS when it has rows <= 32 real rows, or <= 64 at np = 128
+    ("few_rows"), LDS-resident
+    for mp == 128 and np in {128, 256, 512}, the Gram kernel plus the fused
+    GramB/Apply kernel for 512 x 512 tiles, streamed 256-blocks for other
+    multiples of 256, else 128-blocks."""
     if family == "block128":
         return "small"
+    if family == "auto" and rows and 0 < rows <= 64 and mp == 128 and (
+            (rows > 32 and np_ == 128) or (rows <= 32 and np_ in (128, 256, 384, 512, 768, 1024))
+            or (rows <= 16 and np_ in (1536, 2048))):
+        return "few_rows"
     if mp == 128 and np_ in (128, 256, 512):
         return "lds"
     if mp % 256 == 0 and np_ % 256 == 0:
@@ -527,13 +534,14 @@ def ns_rect(reps: int, warmup: int, total_elements: int = 1 << 21) -> list[dict]
             x.copy_(x0)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)
-            nat.ns5(x, y, inv, B, mp, np_, 5, ws, B)
+            nat.ns5(x, y, inv, B, mp, np_, 5, ws, B, rows=m)
             e1.record(s)
             e1.synchronize()
             if k >= warmup:
                 ts.append(e0.elapsed_time(e1))
         ms = float(np.median(ts))
-        out.append({"M": m, "N": n, "B": B, "mp": mp, "np": np_, "family": ns_family(mp, np_), "ms": round(ms, 4),
+        out.append({"M": m, "N": n, "B": B, "mp": mp, "np": np_, "family": ns_family(mp, np_, rows=m),
+                    "ms": round(ms, 4),
                     "GBps": round(B * m * n * 2 / (ms * 1e-3) / 1e9, 1),
                     "tflops": round(ns_flops(m, n) * B / (ms * 1e-3) / 1e12, 2)})
         del x0, x, y, ws
@@ -811,7 +819,7 @@ def main():
     apply_ms = time_apply(opt, reps=max(3, args.steps // 2))
     flops = algorithmic_flops(opt)
     n_tiles = sum(g["tiles"].n_tiles for g in opt._groups)
-    fams = sorted({ns_family(g["tiles"].mp, g["tiles"].np) for g in opt._groups})
+    fams = sorted({ns_family(g["tiles"].mp, g["tiles"].np, rows=g["tiles"].m) for g in opt._groups})
     n_el = sum(p.numel() for p in params)
     # bytes per element: update (untile writes it, the WD/LR pass reads it), parameter;
     # fused: the untile reads the NS tile and reads and writes the parameter

@@ -254,6 +254,26 @@ NS_FAMILY_BLOCK128 = 1
 NS_FAMILY_STREAM3 = 2
 NS_ROUND_ONCE = 0x10
 NS_FAMILIES = {"auto": NS_FAMILY_AUTO, "block128": NS_FAMILY_BLOCK128, "stream3": NS_FAMILY_STREAM3}
+# HIMUON_NS_ROWS(m): the NS operands' real row count, when at most 64 (small-M
+# tiles iterate at their own height instead of the padded mp = 128).
+NS_ROWS_SHIFT = 8
+NS_ROWS_MAX = 64
+
+
+def few_rows_supported(m: int, mp: int, np_: int) -> bool:
+    """Whether family AUTO runs m-row NS operands at their own height (the
+    dispatch rule of himuon_ns5_ex with HIMUON_NS_ROWS(m)): mp == 128, np a
+    multiple of 128 (of 256 above 512) up to 2048 (m <= 16) or 1024
+    (16 < m <= 32); 32 < m <= 64 at np = 128 only."""
+    if mp != 128 or not 0 < m <= NS_ROWS_MAX:
+        return False
+    if m > 32:
+        return np_ == 128
+    if np_ in (128, 256, 384, 512):
+        return True
+    if m <= 32 and np_ in (768, 1024):
+        return True
+    return m <= 16 and np_ in (1536, 2048)
 
 
 def default_sub_batch(n_tiles: int, mp: int, np_: int) -> int:
@@ -304,14 +324,17 @@ def tile_scale(partials, per_tile, n_tiles, inv, eps=NS_EPS):
 
 
 def ns5(x, y, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, NS_B, NS_C), family="auto",
-        round_once=False):
+        round_once=False, rows=0):
     """NS5 on tiles x; X ping-pongs into y: the result is in x for an even
     step count and in y for an odd one. ``family``: a key of NS_FAMILIES;
-    ``round_once`` selects the 2-D rounding of the third product."""
+    ``round_once`` selects the 2-D rounding of the third product; ``rows``: the
+    NS operands' real row count (0: unknown or above NS_ROWS_MAX)."""
     a, b, c = coeffs
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     flags = _stage_flags(family, round_once)
+    if 0 < rows <= NS_ROWS_MAX:
+        flags |= rows << NS_ROWS_SHIFT
     _check(
         load().himuon_ns5_ex(
             x.data_ptr(), y.data_ptr(), inv.data_ptr(), n_tiles, mp, np_, steps, a, b, c,

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIBDIR = PKG / "lib"
 LIB = LIBDIR / "libhimuon_hip.so"
-SOURCES = ["tile_io.hip", "apply.hip", "adamw.hip", "ns5.hip", "ns5_stream.hip", "ns5_lds.hip", "ns5_ba.hip", "products.hip", "capi.hip"]
+SOURCES = ["tile_io.hip", "apply.hip", "adamw.hip", "ns5.hip", "ns5_stream.hip", "ns5_lds.hip", "ns5_ba.hip", "ns5_small.hip", "products.hip", "capi.hip"]
 ARCH = os.environ.get("HIMUON_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

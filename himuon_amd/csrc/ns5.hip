@@ -295,9 +295,10 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
                              size_t workspace_bytes, int64_t sub_batch, int flags, void* stream) {
   const int family = flags & HIMUON_NS_FAMILY_MASK;
   const bool round_once = (flags & HIMUON_NS_ROUND_ONCE) != 0;
+  const int rows = (flags & HIMUON_NS_ROWS_MASK) >> HIMUON_NS_ROWS_SHIFT;
   if (!x || !y || x == y || !inv || n_tiles < 0 || steps < 0 || mp <= 0 || np <= 0 || mp > np ||
-      mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN || sub_batch <= 0 ||
-      (flags & ~(HIMUON_NS_FAMILY_MASK | HIMUON_NS_ROUND_ONCE)) ||
+      mp % HIMUON_NS_ALIGN || np % HIMUON_NS_ALIGN || sub_batch <= 0 || rows > 64 ||
+      (flags & ~(HIMUON_NS_FAMILY_MASK | HIMUON_NS_ROUND_ONCE | HIMUON_NS_ROWS_MASK)) ||
       (family != HIMUON_NS_FAMILY_AUTO && family != HIMUON_NS_FAMILY_BLOCK128 &&
        family != HIMUON_NS_FAMILY_STREAM3))
     return HIMUON_EINVAL;
@@ -326,6 +327,7 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
   // 512 x 512 tiles run the first product on the stream kernels and the
   // other two fused (ns5_ba.hip); family STREAM3 keeps three stream kernels.
   const bool small = family == HIMUON_NS_FAMILY_BLOCK128;
+  const bool few_rows = family == HIMUON_NS_FAMILY_AUTO && ns5_small_supported(rows, mp, np);
   const bool st = ns5_stream_supported(mp, np) && !small;
   const bool lds = ns5_lds_supported(mp, np) && !small;
   const bool ba = ns5_ba_supported(mp, np) && family == HIMUON_NS_FAMILY_AUTO;
@@ -336,7 +338,9 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
   for (int64_t s0 = 0; s0 < n_tiles; s0 += sb) {
     const int64_t cnt = std::min<int64_t>(sb, n_tiles - s0);
     const int64_t o = s0 * rect;
-    if (lds) {
+    if (few_rows) {
+      if (!ns5_small_run(x + o, y + o, inv + s0, cnt, rows, np, steps, a, b, c, round_once, s)) return HIMUON_EINVAL;
+    } else if (lds) {
       ns5_lds_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, s);
     } else if (st) {
       const int rc = ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, ba, wsA,

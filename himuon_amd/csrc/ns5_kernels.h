@@ -196,6 +196,14 @@ bool lds_step_supported(int tile_h, int tile_w, int dtype, int param_dtype);
 void lds_step_run(const HimuonParamDesc* params, int n_params, int64_t tile_begin, int64_t cnt, int tile_h,
                   int tile_w, int dtype, int param_dtype, int steps, float a, float b, float c, float eps,
                   bool round_once, const float* sa, hipStream_t s);
+// NS tiles with m <= 64 real rows in a 128-row padded buffer (ns5_small.hip):
+// the tile's rows 0 .. me - 1 (me = 16, 32 or 64 >= m) iterate in LDS, one
+// workgroup per tile; np = 128 (me = 64), up to 1024 (32) or 2048 (16). Reads
+// x, leaves the result's me rows in x (even `steps`) or y (odd) and touches no
+// other row. False (nothing launched) for an unsupported geometry.
+bool ns5_small_supported(int m, int mp, int np);
+bool ns5_small_run(const uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int m, int np, int steps,
+                   float a, float b, float c, bool round_once, hipStream_t s);
 bool ns5_lds_supported(int mp, int np);
 void ns5_lds_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
                  float a, float b, float c, bool round_once, hipStream_t s);

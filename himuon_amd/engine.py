@@ -212,7 +212,7 @@ class TileGroup:
         nat.ns5(
             r(self.tiles, start, count), r(self.alt, start, count),
             self.inv[start : start + count], count, self.mp, self.np, steps,
-            workspace, sub_batch, family=self.ns_family, round_once=self.round_once,
+            workspace, sub_batch, family=self.ns_family, round_once=self.round_once, rows=self.m,
         )
 
     def lds_step_ok(self) -> bool:

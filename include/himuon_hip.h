@@ -167,6 +167,17 @@ int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles,
  *    128x128-block kernels for every geometry; HIMUON_NS_FAMILY_STREAM3 runs
  *    the three products as three streamed 256-block kernels where AUTO fuses
  *    the second and third (512 x 512 tiles). Results are identical.
+ *  - HIMUON_NS_ROWS(m), m = 1 .. 64: the tiles' NS operands have only m
+ *    nonzero rows (the reference's small-M shapes, e.g. 16 x 1024;
+ *    himuon.py:261-284). With mp == 128, family AUTO then iterates only the
+ *    first 16, 32 or 64 rows (the first that is at least m) of each tile in
+ *    LDS, one workgroup per tile, for np up to 2048 (m <= 16), up to 1024
+ *    (m <= 32) or 128 (m <= 64; wider 64-row tiles run the 128-row kernel,
+ *    measured faster); rows from there to mp are neither read nor written (the result's rows
+ *    below m are those a full computation gives; the rest of y's rows stay
+ *    unspecified). Without it (0), or for other geometries, all mp rows run.
+ *    The same mathematics and rounding points, in another summation order
+ *    than the 128-row kernels (16 x 16 MFMA tiles).
  * Any other flag bit is an argument error.
  */
 #define HIMUON_NS_FAMILY_MASK 0x0F
@@ -174,6 +185,9 @@ int himuon_ns5(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles,
 #define HIMUON_NS_FAMILY_BLOCK128 1
 #define HIMUON_NS_FAMILY_STREAM3 2
 #define HIMUON_NS_ROUND_ONCE 0x10
+#define HIMUON_NS_ROWS_SHIFT 8
+#define HIMUON_NS_ROWS_MASK (0x7F << HIMUON_NS_ROWS_SHIFT)
+#define HIMUON_NS_ROWS(m) ((m) << HIMUON_NS_ROWS_SHIFT)
 int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles,
                   int mp, int np, int steps, float a, float b, float c,
                   void* workspace, size_t workspace_bytes, int64_t sub_batch,

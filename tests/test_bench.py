@@ -31,7 +31,24 @@ def test_ns_family_follows_the_library_dispatch():
     assert bench.ns_family(640, 768) == "small"
     assert bench.ns_family(384, 384) == "small"
     assert bench.ns_family(512, 512, "block128") == "small"
-    assert set(bench.NS_KERNELS) == {"fused", "stream", "lds", "small"}
+    # operands with at most 64 real rows in a 128-row buffer: their own rows in LDS
+    assert bench.ns_family(128, 1024, rows=16) == "few_rows" and bench.ns_family(128, 2048, rows=16) == "few_rows"
+    assert bench.ns_family(128, 1024, rows=32) == "few_rows" and bench.ns_family(128, 2048, rows=32) == "small"
+    assert bench.ns_family(128, 128, rows=64) == "few_rows" and bench.ns_family(128, 512, rows=64) == "lds"
+    assert bench.ns_family(128, 1024, rows=64) == "small" and bench.ns_family(128, 384, rows=40) == "small"
+    assert bench.ns_family(128, 384, rows=20) == "few_rows" and bench.ns_family(128, 128, rows=100) == "lds"
+    assert bench.ns_family(128, 1024, "block128", rows=16) == "small"
+    assert set(bench.NS_KERNELS) == {"fused", "stream", "lds", "small", "few_rows"}
+
+
+def test_few_rows_rule_matches_the_binding():
+    from himuon_amd import _native as nat
+
+    for m in (1, 16, 17, 32, 33, 48, 64, 65, 128):
+        for np_ in (128, 256, 384, 512, 640, 768, 1024, 1536, 2048, 4096):
+            expect = nat.few_rows_supported(m, 128, np_)
+            assert (bench.ns_family(128, np_, rows=m) == "few_rows") == expect, (m, np_)
+    assert not nat.few_rows_supported(16, 256, 1024)
 
 
 def test_ns_flops_is_the_normative_count():

@@ -240,14 +240,20 @@ def test_ns5_singular_value_band(T, n, ns_family):
 def test_ns5_zero_tile_and_padding(ns_family):
     # zero tiles map to zero (0 / (0 + eps) = 0); zero padding stays zero and
     # does not change the data block (a 37x100 block in a 256x256 tile equals
-    # the same block NS'd in its own 128x128 padding, bit for bit)
+    # the same block NS'd in its own 128x128 padding, bit for bit, with the
+    # 128-row kernels; AUTO runs a 37-row tile at 64 rows on 16 x 16 MFMA
+    # tiles, another summation order: within the per-tile bar)
     G = torch.zeros(3, 256, 256, device=DEV)
     G[1, :37, :100] = _cpu_randn((37, 100), 4).to(DEV)
     out = _ns_engine(G, family=ns_family)
     assert (out[0] == 0).all() and (out[2] == 0).all()
     assert (out[1, 37:] == 0).all() and (out[1, :, 100:] == 0).all()
-    small = _ns_engine(G[1:2, :37, :100].contiguous(), family=ns_family)
+    blk = "block128" if ns_family == "auto" else ns_family
+    small = _ns_engine(G[1:2, :37, :100].contiguous(), family=blk)
     assert torch.equal(out[1, :37, :100], small[0])
+    if ns_family == "auto":
+        few = _ns_engine(G[1:2, :37, :100].contiguous())
+        assert per_tile_rel_fro(few, small).max() <= 1e-2
 
 
 @pytest.mark.parametrize("shape", [(2, 256, 512), (2, 128, 128), (2, 128, 256), (2, 128, 512)],
@@ -288,6 +294,8 @@ STALE_SHAPES = [
     ("stream_256", 3, 256, 256),
     ("stream_200x500", 2, 200, 500),
     ("stream_tall_1000x400", 2, 1000, 400),
+    ("few_rows_16x1024", 3, 16, 1024),
+    ("few_rows_tall_300x40", 2, 300, 40),
 ]
 
 
@@ -357,3 +365,41 @@ def test_ns5_many_tiles_large_buffers():
     print(f"  sampled tiles vs staged torch: max {err.max():.4f} mean {err.mean():.4f}", flush=True)
     assert err.max() <= 1e-2
     assert torch.equal(out[idx], ref)
+
+
+FEW_ROWS = [(8, 16, 1024), (4, 32, 512), (4, 64, 128), (6, 16, 128), (3, 1, 300), (2, 5, 2048), (2, 48, 100),
+            (3, 20, 640), (2, 32, 1024), (2, 1024, 16), (16, 1024), (4, 64, 256)]
+
+
+@pytest.mark.parametrize("shape", FEW_ROWS, ids=["x".join(map(str, s)) for s in FEW_ROWS])
+@pytest.mark.parametrize("steps", [1, 2, 5])
+def test_ns5_few_rows(shape, steps):
+    """NS operands of m <= 64 rows iterate at 16, 32 or 64 rows (HIMUON_NS_ROWS;
+    the reference's small-M shapes, himuon.py:261-284), on 16 x 16 MFMA tiles,
+    one workgroup per tile. Against torch's same-dtype NS5: per-tile relative
+    Frobenius <= 1e-2 (the north star's bar; another summation order than
+    torch's, so not bit for bit), as the 128-row kernels on the padded tiles;
+    against the numpy oracle at the noise floor; singular values in
+    the quintic's band. Odd and even step counts (result in either buffer), a
+    tall input (transposed) and a 2-D one (the addmm rounding)."""
+    print(f"[ns5 few rows] {shape} steps={steps}", flush=True)
+    G = _cpu_randn(shape, seed=sum(shape) + steps, scale=1e-3).to(DEV)
+    out = newton_schulz(G, steps=steps)
+    ref = ns5_torch_staged(G, steps=steps, round_once=G.ndim == 2)
+    blk = newton_schulz(G, steps=steps, family="block128")  # all 128 padded rows
+    assert out.shape == G.shape and torch.isfinite(out).all()
+    err = per_tile_rel_fro(out, ref)
+    assert per_tile_rel_fro(blk, ref).max() <= 1e-2
+    ref_o = O.ns5_staged_2d(G.cpu().numpy(), steps=steps) if G.ndim == 2 else O.ns5_staged(G.cpu().numpy(), steps=steps)
+    e_o = per_tile_rel_fro(out, torch.from_numpy(ref_o).to(DEV))
+    print(f"  vs torch max {err.max():.2e}, vs oracle max {e_o.max():.2e}", flush=True)
+    assert err.max() <= 1e-2
+    assert e_o.mean() <= 1e-2 and e_o.max() <= 2e-2
+    if steps == 5:
+        g3 = G.reshape(-1, *G.shape[-2:]).double()
+        sv = torch.linalg.svdvals(out.reshape(g3.shape).double()).cpu().numpy()
+        sv_in = torch.linalg.svdvals(g3).cpu().numpy()
+        sv_in = sv_in / np.linalg.norm(g3.cpu().numpy(), axis=(-2, -1))[:, None]
+        for k in range(sv.shape[0]):
+            lo, hi = O.quintic_band(max(sv_in[k].min(), 4e-3), sv_in[k].max())
+            assert sv[k].max() <= hi + 0.03 and sv[k].min() >= lo - 0.03
