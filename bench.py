@@ -548,9 +548,157 @@ def ns_rect(reps: int, warmup: int, total_elements: int = 1 << 21) -> list[dict]
     return out
 
 
+# The reference's optimizer step microbenchmark
+# (microbench/experiments/exp_optimizer_step_microbench.py:58-86,123-164):
+# 8 x Linear(H, H) bf16 parameters with bf16 grads ~N(0, 1) refilled before
+# every step, HiMuon at tile 512 with graph capture (warm-up 3) against Muon
+# (full-matrix NS); median of 50 steps after 20, HIP events around each step;
+# peak memory over 5 steps after 5. Its figure (a) reports Muon / HiMuon
+# step-time ratios of 2.3 / 3.7 / 5.4 at H = 1024 / 2048 / 4096 on unstated
+# NVIDIA hardware (read off microbench/plots/optimizer_step_microbench.png).
+# Muon here is this library's full-matrix mode (tile_size above the matrix:
+# NS on each whole matrix, same-shape matrices batched), the reference's
+# Muon update on the same kernels.
+STEP_MICRO_H = {"step-8xh1024": 1024, "step-8xh2048": 2048, "step-8xh4096": 4096}
+STEP_MICRO_REF_RATIO = {1024: 2.3, 2048: 3.7, 4096: 5.4}
+
+
+def step_micro(H: int, reps: int, warmup: int, K: int = 8) -> dict:
+    from himuon_amd.optimizers.himuon import HiMuon
+
+    res = {}
+    for label, tile in (("himuon_tile512", 512), ("muon_full_matrix", 1_000_000_000)):
+        torch.cuda.empty_cache()
+        torch.manual_seed(7)
+        params = []
+        for _ in range(K):
+            p = torch.nn.Parameter(torch.empty(H, H, device="cuda", dtype=torch.bfloat16))
+            torch.nn.init.kaiming_uniform_(p, a=5 ** 0.5)  # nn.Linear's init
+            params.append(p)
+        opt = HiMuon([{"params": params, "weight_decay": 0.0, "use_muon": True}], lr=0.02, momentum=0.95,
+                     nesterov=True, weight_decay=0.1, tile_size=tile, ns_steps=5, cuda_graph=True,
+                     cuda_graph_warmup=3)
+        gen = torch.Generator(device="cuda")
+
+        def fill(seed):
+            gen.manual_seed(seed)
+            for p in params:
+                if p.grad is None:
+                    p.grad = torch.empty_like(p)
+                p.grad.normal_(generator=gen)
+
+        for i in range(warmup):
+            fill(5000 + i)
+            opt.step()
+        torch.cuda.synchronize()
+        times = []
+        for i in range(reps):
+            fill(5000 + warmup + i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            opt.step()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        for i in range(5):
+            fill(9000 + i)
+            opt.step()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        for i in range(5):
+            fill(9100 + i)
+            opt.step()
+        torch.cuda.synchronize()
+        res[label] = {"ms_median": round(float(np.median(times)), 4),
+                      "ms_p25_p75": [round(float(np.percentile(times, q)), 4) for q in (25, 75)],
+                      "peak_mem_bytes": int(torch.cuda.max_memory_allocated())}
+        del opt, params
+    ratio = res["muon_full_matrix"]["ms_median"] / res["himuon_tile512"]["ms_median"]
+    mem = res["himuon_tile512"]["peak_mem_bytes"] / res["muon_full_matrix"]["peak_mem_bytes"] - 1.0
+    return {"H": H, "K": K, **res, "speedup_vs_muon": round(ratio, 3), "peak_mem_vs_muon": round(mem, 4),
+            "reference_speedup_vs_muon": STEP_MICRO_REF_RATIO.get(H)}
+
+
+# The reference's per-layer tile-NS vs full-NS benchmark
+# (microbench/experiments/exp_real_shapes_bench.py:43-50,125-160): for each
+# Muon-eligible weight shape of a Qwen3 transformer block, G ~ randn bf16;
+# tile NS = HiMuon._tile -> newton_schulz on the (R C, T, T) batch ->
+# HiMuon._untile (the torch tiling copies included, as there), full NS =
+# NS of the whole matrix (there Muon's zeropower_via_newtonschulz5, here this
+# library's 2-D newton_schulz); median of 30 calls after 3, HIP events. Its
+# figure reports tile/full speed-ups of 1.4-1.6x (Qwen3-0.6B) and 1.3x (k/v)
+# to 2.9x (q) (Qwen3-4B) on unstated NVIDIA hardware
+# (microbench/plots/real_shapes_bench.png).
+REAL_SHAPES = {
+    "real-shapes-qwen3-0.6b": [("q_proj", (2048, 1024)), ("k_proj", (1024, 1024)), ("v_proj", (1024, 1024)),
+                               ("o_proj", (1024, 2048)), ("gate_proj", (3072, 1024)), ("up_proj", (3072, 1024)),
+                               ("down_proj", (1024, 3072))],
+    "real-shapes-qwen3-4b": [("q_proj", (4096, 2560)), ("k_proj", (1024, 2560)), ("v_proj", (1024, 2560)),
+                             ("o_proj", (2560, 4096)), ("gate_proj", (9728, 2560)), ("up_proj", (9728, 2560)),
+                             ("down_proj", (2560, 9728))],
+}
+
+
+def real_shapes(config: str, reps: int, warmup: int, tile: int = 512) -> list[dict]:
+    from himuon_amd.optimizers.himuon import HiMuon
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return float(np.median(ts))
+
+    rows = []
+    for name, (h, w) in REAL_SHAPES[config]:
+        torch.manual_seed(0)
+        G = torch.randn(h, w, device="cuda", dtype=torch.bfloat16)
+
+        def tile_ns():
+            tiled, info = HiMuon._tile(G, (tile, tile))
+            R, C, Th, Tw = tiled.shape
+            orth = HiMuon.newton_schulz(tiled.view(-1, Th, Tw), steps=5).view(R, C, Th, Tw)
+            return HiMuon._untile(orth, info)
+
+        def full_ns():
+            return HiMuon.newton_schulz(G.clone(), steps=5)
+
+        t_tile, t_full = timed(tile_ns), timed(full_ns)
+        m, n = min(h, w), max(h, w)
+        R, C = -(-h // tile), -(-w // tile)
+        rows.append({"layer": name, "shape": [h, w], "tiles": R * C, "tile_ms": round(t_tile, 4),
+                     "full_ms": round(t_full, 4), "speedup": round(t_full / t_tile, 3),
+                     "full_ns_tflops": round(ns_flops(m, n) / (t_full * 1e-3) / 1e12, 1),
+                     "tile_ns_tflops": round(R * C * ns_flops(tile, tile) / (t_tile * 1e-3) / 1e12, 1)})
+    return rows
+
+
 def ns_micro_line(args) -> dict:
     """The JSON line of an NS microbenchmark config."""
     warmup = max(args.warmup, 2)
+    if args.config in STEP_MICRO_H:
+        r = step_micro(STEP_MICRO_H[args.config], args.steps, args.warmup)
+        return {"metric": "HiMuon step time (ms), 8 x Linear(H, H) bf16, tile 512, against full-matrix NS (Muon)",
+                "value": r["himuon_tile512"]["ms_median"], "unit": "ms", "n_gpus": 1, "steps": args.steps,
+                "warmup": args.warmup, "ms_per_step": r["himuon_tile512"]["ms_median"], "higher_is_better": False,
+                "scaling": "strong", "vs_baseline": None, "dtype": "bf16",
+                "data": "synthetic: nn.Linear init, bf16 grads ~N(0, 1) refilled per step",
+                "config": {"workload": args.config, "H": r["H"], "K": r["K"]}, "result": r}
+    if args.config in REAL_SHAPES:
+        rows = real_shapes(args.config, args.steps, warmup)
+        return {"metric": "NS5 time per call (ms), tile 512 vs full matrix, per layer shape",
+                "value": round(sum(r["tile_ms"] for r in rows), 4), "unit": "ms (sum of tile-NS over layers)",
+                "n_gpus": 1, "steps": args.steps, "warmup": warmup, "higher_is_better": False,
+                "scaling": "strong", "vs_baseline": None, "dtype": "bf16", "data": "synthetic: torch.randn bf16",
+                "config": {"workload": args.config, "tile": 512}, "layers": rows}
     if args.config == "ns-rect":
         rows = ns_rect(args.steps, warmup)
         return {"metric": "NS5 time per call (ms) over the reference's (M, N) tile-shape sweep",
@@ -732,10 +880,14 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS) + sorted(NS_MICRO_B) + ["ns-rect"],
-                    help="a parameter-set config (the HiMuon step), or an NS microbenchmark of the reference's: "
-                         "ns-t128-b{32,128,512,2048} (NS5 per call on B tiles of 128x128; also b65536) or ns-rect "
-                         "(its rectangular tile-shape sweep)")
+    ap.add_argument("--config", default="qwen3-4b",
+                    choices=sorted(CONFIGS) + sorted(NS_MICRO_B) + ["ns-rect"] + sorted(STEP_MICRO_H)
+                    + sorted(REAL_SHAPES),
+                    help="a parameter-set config (the HiMuon step), or a microbenchmark of the reference's: "
+                         "ns-t128-b{32,128,512,2048} (NS5 per call on B tiles of 128x128; also b65536), ns-rect "
+                         "(its rectangular tile-shape sweep), step-8xh{1024,2048,4096} (8 x Linear(H, H) step, "
+                         "tile 512 against full-matrix NS) or real-shapes-qwen3-{0.6b,4b} (per-layer tile-NS "
+                         "against full-NS)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-adamw", action="store_true",
                     help="skip the AdamW fallback timing (Qwen3-4B embedding, fused vs torch ops)")
@@ -764,7 +916,8 @@ def main():
     from himuon_amd.optimizers.himuon import HiMuon
 
     load()
-    if args.config in NS_MICRO_B or args.config == "ns-rect":
+    if args.config in NS_MICRO_B or args.config in STEP_MICRO_H or args.config in REAL_SHAPES \
+            or args.config == "ns-rect":
         print(json.dumps(ns_micro_line(args)), flush=True)
         return
     # A 256 MiB device copy of known size: under `rocprofv3 --pmc` its

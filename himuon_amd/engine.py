@@ -343,10 +343,12 @@ class AdamwTables:
 class _NsPlan:
     """Device state of ``newton_schulz`` for one (batch shape, dtype, device,
     rounding form, kernel family): a tile group over its own input and output
-    buffers, the sub-batch and the NS workspace, built once. A call copies the
-    input into ``xin`` and the result out of ``out``, so it neither allocates
-    device state (beyond the returned tensor) nor rewrites the descriptor
-    table, and repeated calls cost only the launches."""
+    buffers, the sub-batch and the NS workspace, built once, and per step
+    count a hipGraph of its launches (gather, normaliser, NS, untile),
+    captured on first use. A call copies the input into ``xin``, replays the
+    graph and copies the result out of ``out``: it neither allocates device
+    state (beyond the returned tensor) nor rewrites the descriptor table, and
+    costs one replay instead of a dozen or more host launches."""
 
     def __init__(self, n: int, M: int, N: int, dtype: torch.dtype, device, round_once: bool, family: str):
         self.xin = torch.empty((n * M, N), device=device, dtype=dtype)
@@ -357,12 +359,31 @@ class _NsPlan:
         self.out = self.grp.updates[0]
         self.sub_batch = self.grp.default_sub_batch()
         self.ws = torch.empty(max(1, self.grp.workspace_bytes(self.sub_batch)), device=device, dtype=torch.uint8)
+        self.grp.tiles  # allocate the tile buffers now, not inside a capture
+        self.graphs: "dict[int, torch.cuda.CUDAGraph]" = {}
+        # recorded into a caller's graph: that graph holds these buffers'
+        # addresses, so the plan is never dropped
+        self.pinned = False
 
-    def run(self, steps: int) -> torch.Tensor:
+    def _launches(self, steps: int) -> None:
         g = self.grp
         g.gather()
         g.ns(0, g.n_tiles, steps, self.ws, self.sub_batch)
         g.untile(steps)
+
+    def run(self, steps: int) -> torch.Tensor:
+        if torch.cuda.is_current_stream_capturing():
+            # inside the caller's capture: record the launches there
+            self.pinned = True
+            self._launches(steps)
+            return self.out
+        graph = self.graphs.get(steps)
+        if graph is None:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._launches(steps)
+            self.graphs[steps] = graph
+        graph.replay()
         return self.out
 
 
@@ -379,7 +400,8 @@ def newton_schulz(G: torch.Tensor, steps: int = 5, family: str = "auto") -> torc
     the reference's 2-D rounding of the third product (torch.addmm,
     himuon.py:249-253); a batched one that of fused_bmm_add. The device state
     for a shape is built on its first call and reused (at most _NS_PLANS_MAX
-    shapes are kept, the oldest dropped first); the result is a new tensor.
+    shapes are kept, the least recently used dropped first, except those
+    recorded into a caller's graph); the result is a new tensor.
     ``family``: the NS kernel family (comparison runs; "auto" otherwise)."""
     assert G.ndim >= 2
     if not G.is_cuda:
@@ -393,7 +415,9 @@ def newton_schulz(G: torch.Tensor, steps: int = 5, family: str = "auto") -> torc
     plan = _NS_PLANS.pop(key, None)
     if plan is None:
         if len(_NS_PLANS) >= _NS_PLANS_MAX:
-            _NS_PLANS.pop(next(iter(_NS_PLANS)))
+            old = next((k for k, v in _NS_PLANS.items() if not v.pinned), None)
+            if old is not None:
+                _NS_PLANS.pop(old)
         plan = _NsPlan(n, M, N, dtype, G.device, G.ndim == 2, family)
     _NS_PLANS[key] = plan  # most recently used last
     plan.xin.view(G.shape).copy_(G)

@@ -403,3 +403,35 @@ def test_ns5_few_rows(shape, steps):
         for k in range(sv.shape[0]):
             lo, hi = O.quintic_band(max(sv_in[k].min(), 4e-3), sv_in[k].max())
             assert sv[k].max() <= hi + 0.03 and sv[k].min() >= lo - 0.03
+
+
+def test_newton_schulz_replays_and_captures():
+    """newton_schulz keeps its device state per shape and replays a graph of
+    its launches per step count: consecutive calls with new inputs (and
+    another step count) equal the launches run eagerly on the same inputs,
+    the inputs are not modified, each call returns a new tensor; and the call
+    can itself be recorded into a caller's graph and replayed."""
+    from himuon_amd import engine as E
+
+    shape = (6, 256, 512)
+    gs = [_cpu_randn(shape, seed=70 + k, scale=1e-3).to(DEV) for k in range(3)]
+    keep = [g.clone() for g in gs]
+    outs = [newton_schulz(gs[0]), newton_schulz(gs[1]), newton_schulz(gs[2], steps=3), newton_schulz(gs[0])]
+    for g, k in zip(gs, keep):
+        assert torch.equal(g, k)
+    assert outs[0].data_ptr() != outs[3].data_ptr() and torch.equal(outs[0], outs[3])
+    for out, g, st in zip(outs, (gs[0], gs[1], gs[2]), (5, 5, 3)):
+        plan = E._NsPlan(shape[0], shape[1], shape[2], torch.float32, g.device, False, "auto")
+        plan.xin.view(shape).copy_(g)
+        plan._launches(st)
+        assert torch.equal(out, plan.out.view(shape))
+    # recorded into a caller's capture (launches, not a nested replay)
+    static_in = gs[1].clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = newton_schulz(static_in)
+    for k in range(3):
+        static_in.copy_(gs[k])
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, newton_schulz(gs[k]))
