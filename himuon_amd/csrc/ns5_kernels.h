@@ -88,9 +88,12 @@ HM_DEV void wait_lgkm() {
 // compiler cannot tell these reads apart from the direct-to-LDS loads in
 // flight and would put a vmcnt(0) wait (draining the operand stream) before
 // the builtin. The result is only valid after an explicit lgkmcnt wait.
+// OFF: the instruction's immediate byte offset (0 .. 65535).
+template <int OFF = 0>
 HM_DEV u32x2_t ds_read_tr16(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "DS offset range");
   u32x2_t r;
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
   return r;
 }
 

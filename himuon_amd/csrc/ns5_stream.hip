@@ -242,7 +242,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   const int tr_s = swz_x(te);
   const int tr_row = 8 * hi + te;
   const int tr_chunk = wn * (WC / 8) + 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
-  const int tr_sub = (r16 & 1) * 8;
+  const uint32_t tr_lane = (uint32_t)(uintptr_t)lds + HALF + tr_row * 512 + (r16 & 1) * 8;
   // which: 1 = P fragments (fb), 2 = Q fragments (fa), 3 = both.
   auto frags = [&](int v, int ks, u32x4_t(&fa)[TJ], u32x4_t(&fb)[4], int which = 3) {
     const lds_u8* s = lds + (v % NSLOT) * SLOT;
@@ -252,12 +252,18 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
       for (int t = 0; t < 4; ++t) fb[t] = *reinterpret_cast<lds_cu32x4*>(s + prow + t * 2048 + pos);
     }
     if (!(which & 2)) return;
+    // Apply: the lane's read base is made opaque per call, so the addresses
+    // of equal (slot, ks) in different units of the unrolled K loop are not
+    // merged and kept live across units; rows 4 .. 7 of a read pair come from
+    // the instruction's offset field.
+    uint32_t trb = tr_lane;
+    if constexpr (kTr) asm volatile("" : "+v"(trb));
+    trb += (v % NSLOT) * SLOT + 16 * ks * 512;
 #pragma unroll
     for (int t = 0; t < TJ; ++t) {
       if constexpr (kTr) {
-        const uint32_t off = (uint32_t)(uintptr_t)s + HALF + (16 * ks + tr_row) * 512 +
-                             (((tr_chunk + 4 * t) ^ tr_s) * 16) + tr_sub;
-        const u32x2_t l2 = ds_read_tr16(off), u2 = ds_read_tr16(off + 4 * 512);
+        const uint32_t off = trb + (((tr_chunk + 4 * t) ^ tr_s) * 16);
+        const u32x2_t l2 = ds_read_tr16(off), u2 = ds_read_tr16<4 * 512>(off);
         fa[t] = u32x4_t{l2[0], l2[1], u2[0], u2[1]};
       } else {
         const lds_u8* qs = DIAG ? s : s + HALF;
