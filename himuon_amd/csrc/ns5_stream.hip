@@ -449,6 +449,9 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     for (int v = 0; v < DIST; ++v) issue_k<NW>(ns, wdst, v, v, nx.diag);
   }
 
+  // Output stores are non-temporal: the block is not read again by this
+  // launch, and its lines should not displace operand rows other workgroups
+  // of the XCD still stream from L2.
   // Staging in 4 rounds per block: each wave stages 32 rows x WC columns
   // (WC * 2-byte rows) in its 1/NW of slot DIST, then stores them with
   // 16-byte lanes, whole rows per instruction: 8 (NW = 4) or 4 (NW = 8)
@@ -477,7 +480,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
       for (int n = 0; n < 32 / RPI; ++n) {
         const int r = RPI * n + srow;
         const u32x4_t v = *reinterpret_cast<lds_cu32x4*>(W + r * RB + ((sch ^ swz_s(r)) * 16));
-        *reinterpret_cast<u32x4_t*>(dst + (int64_t)r * g.ldc + sch * 8) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(dst + (int64_t)r * g.ldc + sch * 8));
       }
     }
   }
@@ -508,7 +511,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
         for (int n = 0; n < MR / 4; ++n) {
           const int r = 4 * n + srow;
           const u32x4_t v = *reinterpret_cast<lds_cu32x4*>(W + r * 256 + ((sch ^ swz_c(r)) * 16));
-          *reinterpret_cast<u32x4_t*>(dst + (int64_t)r * g.ldc + sch * 8) = v;
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(dst + (int64_t)r * g.ldc + sch * 8));
         }
       }
     }
