@@ -18,7 +18,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libhimuon_hip.so"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 NS_ALIGN = 128
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 # Operand dtypes of the typed stage products (himuon_*_typed): the above and fp8 e5m2.
@@ -142,6 +142,12 @@ _SIGNATURES = {
     "himuon_untile": (
         c_int,
         [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p],
+    ),
+    "himuon_ns5_untile_apply_supported": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
+    "himuon_ns5_untile_apply": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_float, c_float, c_float, c_void_p,
+         c_size_t, c_int64, c_int, c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_void_p],
     ),
     "himuon_untile_apply": (
         c_int,
@@ -332,15 +338,50 @@ def ns5(x, y, inv, n_tiles, mp, np_, steps, workspace, sub_batch, coeffs=(NS_A, 
     a, b, c = coeffs
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    flags = _stage_flags(family, round_once)
-    if 0 < rows <= NS_ROWS_MAX:
-        flags |= rows << NS_ROWS_SHIFT
+    flags = _ns_flags(family, round_once, rows)
     _check(
         load().himuon_ns5_ex(
             x.data_ptr(), y.data_ptr(), inv.data_ptr(), n_tiles, mp, np_, steps, a, b, c,
             ws_ptr, ws_bytes, sub_batch, flags, _stream(),
         ),
         "himuon_ns5",
+    )
+
+
+def _ns_flags(family, round_once, rows) -> int:
+    flags = _stage_flags(family, round_once)
+    if 0 < rows <= NS_ROWS_MAX:
+        flags |= rows << NS_ROWS_SHIFT
+    return flags
+
+
+def ns5_untile_apply_supported(mp, np_, tile_h, tile_w, steps, param_dtype, family="auto", round_once=False):
+    """True when himuon_ns5_untile_apply takes this geometry (512 x 512 NS
+    tiles, not transposed, family AUTO, steps >= 2, fp32 or bf16 parameters)."""
+    if param_dtype not in DTYPE_CODES:
+        return False
+    return bool(load().himuon_ns5_untile_apply_supported(mp, np_, tile_h, tile_w, steps,
+                                                         _stage_flags(family, round_once),
+                                                         DTYPE_CODES[param_dtype]))
+
+
+def ns5_untile_apply(x, y, inv, n_tiles, mp, np_, steps, workspace, sub_batch, desc_table, n_params, tile_begin,
+                     tile_h, tile_w, param_dtype, scale_alpha, coeffs=(NS_A, NS_B, NS_C), family="auto",
+                     round_once=False, rows=0):
+    """NS5 of bucket tiles tile_begin .. tile_begin + n_tiles - 1 (x, y: the
+    tile buffers advanced to tile_begin) with the untile with the WD/LR of
+    scale_alpha fused into the last iteration: the parameters the descriptors
+    point at are updated in place; x and y hold no NS result afterwards."""
+    a, b, c = coeffs
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(
+        load().himuon_ns5_untile_apply(
+            x.data_ptr(), y.data_ptr(), inv.data_ptr(), n_tiles, mp, np_, steps, a, b, c, ws_ptr, ws_bytes,
+            sub_batch, _ns_flags(family, round_once, rows), desc_table.data_ptr(), n_params, tile_begin, tile_h,
+            tile_w, dtype_code(param_dtype), scale_alpha.data_ptr(), _stream(),
+        ),
+        "himuon_ns5_untile_apply",
     )
 
 

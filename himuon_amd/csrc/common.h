@@ -17,11 +17,12 @@
 // ---------------------------------------------------------------------------
 HM_DEV float bf16_to_f32(uint32_t v) { return __uint_as_float(v << 16); }
 
+// The hardware conversion (v_cvt_pk_bf16_f32, round to nearest even) and the
+// canonical quiet NaN 0x7fc0 for every NaN input.
 HM_DEV uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // canonical quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const __bf16 h = (__bf16)f;
+  const uint32_t b = (uint32_t)__builtin_bit_cast(uint16_t, h);
+  return f != f ? 0x7fc0u : b;
 }
 
 // Round an fp32 value to the nearest bf16 and return it as fp32.

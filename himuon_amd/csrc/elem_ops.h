@@ -23,6 +23,29 @@ HM_DEV float momentum_elem(float g, float* m, float mu, bool nesterov, bool has_
   return round_to<DT>(__builtin_fmaf(mu, mb, g));
 }
 
+// The WD/LR step of the fused untile (himuon_untile_apply, and the fused NS
+// kernel's last iteration) on parameter values p and their updates y:
+//     p = rd(fma(alpha, rd(y), rd(p s)))
+// wdlr8: 8 values p already loaded as fp32 (rounded to DT by the store that
+// follows); wdlr_elems: the first `valid` elements at base + o, one at a time.
+template <int DT>
+HM_DEV void wdlr8(float (&p)[8], const float (&y)[8], float s, float alpha) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = __builtin_fmaf(alpha, round_to<DT>(y[e]), round_to<DT>(p[e] * s));
+}
+template <int DT>
+HM_DEV void wdlr_elems(void* base, int64_t o, const float (&y)[8], int valid, float s, float alpha) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {  // (static indices: y stays in registers)
+    if (e < valid) {
+      const float p1 = round_to<DT>(load_elem<DT>(base, o + e) * s);
+      store_elem<DT>(base, o + e, __builtin_fmaf(alpha, round_to<DT>(y[e]), p1));
+    }
+  }
+}
+
 // Untile store of 8 consecutive update values y (fp32, already scaled by the
 // parameter's upd_scale) at element offset o of descriptor P's `update`;
 // `full`: all 8 in range and 16-byte aligned, else the first `valid` one at a
@@ -40,14 +63,10 @@ HM_DEV void put8(const HimuonParamDesc& P, int64_t o, const float (&y)[8], bool 
     if (full) {
       float p[8];
       load8<DT>(P.update, o, p);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) p[e] = __builtin_fmaf(alpha, round_to<DT>(y[e]), round_to<DT>(p[e] * s));
+      wdlr8<DT>(p, y, s, alpha);
       store8<DT>(P.update, o, p);
     } else {
-      for (int e = 0; e < valid; ++e) {
-        const float p1 = round_to<DT>(load_elem<DT>(P.update, o + e) * s);
-        store_elem<DT>(P.update, o + e, __builtin_fmaf(alpha, round_to<DT>(y[e]), p1));
-      }
+      wdlr_elems<DT>(P.update, o, y, valid, s, alpha);
     }
   } else {
     if (full) {

@@ -290,9 +290,13 @@ extern "C" size_t himuon_ns5_workspace_bytes(int64_t sub_batch, int mp, int np) 
   return 2 * (size_t)sub_batch * mp * mp * sizeof(uint16_t);  // A and B per sub-batch tile
 }
 
-extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp,
-                             int np, int steps, float a, float b, float c, void* workspace,
-                             size_t workspace_bytes, int64_t sub_batch, int flags, void* stream) {
+namespace {
+// himuon_ns5_ex, and with `untile` (himuon_ns5_untile_apply; the caller has
+// checked that the fused path applies) the untile with WD/LR fused into the
+// last iteration: its tile0 is the bucket index of tile 0 of x.
+int ns5_impl(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp, int np, int steps, float a,
+             float b, float c, void* workspace, size_t workspace_bytes, int64_t sub_batch, int flags,
+             void* stream, const BaUntile* untile) {
   const int family = flags & HIMUON_NS_FAMILY_MASK;
   const bool round_once = (flags & HIMUON_NS_ROUND_ONCE) != 0;
   const int rows = (flags & HIMUON_NS_ROWS_MASK) >> HIMUON_NS_ROWS_SHIFT;
@@ -343,8 +347,13 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
     } else if (lds) {
       ns5_lds_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, s);
     } else if (st) {
+      BaUntile u{};
+      if (untile) {
+        u = *untile;
+        u.tile0 += s0;
+      }
       const int rc = ns5_stream_run(x + o, y + o, inv + s0, cnt, mp, np, steps, a, b, c, round_once, ba, wsA,
-                                    wsB, s);
+                                    wsB, s, untile ? &u : nullptr);
       if (rc) return rc;
     } else {
       const uint16_t* cur = x + o;
@@ -370,6 +379,36 @@ extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t
     if (e != hipSuccess) return (int)e;
   }
   return 0;
+}
+}  // namespace
+
+extern "C" int himuon_ns5_ex(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp,
+                             int np, int steps, float a, float b, float c, void* workspace,
+                             size_t workspace_bytes, int64_t sub_batch, int flags, void* stream) {
+  return ns5_impl(x, y, inv, n_tiles, mp, np, steps, a, b, c, workspace, workspace_bytes, sub_batch, flags, stream,
+                  nullptr);
+}
+
+extern "C" int himuon_ns5_untile_apply_supported(int mp, int np, int tile_h, int tile_w, int steps, int flags,
+                                                 int param_dtype) {
+  const int family = flags & HIMUON_NS_FAMILY_MASK;
+  return ns5_ba_supported(mp, np) && family == HIMUON_NS_FAMILY_AUTO && steps >= 2 && tile_h >= 1 &&
+         tile_h <= tile_w && tile_w <= np && tile_h <= mp &&
+         (param_dtype == HIMUON_DTYPE_F32 || param_dtype == HIMUON_DTYPE_BF16);
+}
+
+extern "C" int himuon_ns5_untile_apply(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp, int np,
+                                       int steps, float a, float b, float c, void* workspace,
+                                       size_t workspace_bytes, int64_t sub_batch, int flags,
+                                       const HimuonParamDesc* params_dev, int n_params, int64_t tile_begin,
+                                       int tile_h, int tile_w, int param_dtype, const float* scale_alpha_dev,
+                                       void* stream) {
+  if (!himuon_ns5_untile_apply_supported(mp, np, tile_h, tile_w, steps, flags, param_dtype) || !params_dev ||
+      n_params <= 0 || tile_begin < 0 || !scale_alpha_dev)
+    return HIMUON_EINVAL;
+  const BaUntile u{params_dev, n_params, tile_begin, tile_h, tile_w, param_dtype, scale_alpha_dev};
+  return ns5_impl(x, y, inv, n_tiles, mp, np, steps, a, b, c, workspace, workspace_bytes, sub_batch, flags, stream,
+                  &u);
 }
 
 // ---------------------------------------------------------------------------

@@ -72,6 +72,7 @@
 // c ^ 4 ((r / 2) % 2), conflict-free for the row writes and the transposing
 // reads); in the epilogue one block of 32 rows x 128 B, chunk c of row r at
 // c ^ (r / 2) % 8.
+#include "elem_ops.h"
 #include "ns5_kernels.h"
 
 namespace {
@@ -98,6 +99,7 @@ struct BaArgs {
   float a, b, c;
   int round_once;
   const float* xinv;   // SC: X is the raw tile, X0 = bf16(X xinv[tile]) used in its place
+  BaUntile u;          // the fused untile of the last iteration (kernels with UDT >= 0)
 };
 
 typedef __attribute__((address_space(3))) u32x4_t lds_u32x4;
@@ -121,6 +123,179 @@ HM_DEV void gstore16(uint16_t* base, uint32_t off, u32x4_t v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(base) + off));
 }
 
+// ---- the fused untile of the last NS iteration (kernels with UDT >= 0) -------------
+// Per-tile record of the launch's tiles, written by untile_rec_kernel before
+// the fused kernel runs (16 int32 per tile, the parameter's descriptor found
+// once per tile instead of once per work item and wave):
+//   0-1 parameter base  2-3 row stride  4-5 rows h  6-7 columns w
+//   8-9 parameter row of the tile's (0, 0)  10-11 its column  12 upd_scale bits  13 group
+constexpr int kRecInts = 16;
+static_assert(2 * HIMUON_APPLY_MAX_GROUPS == 64, "one (scale, alpha) value per lane");
+
+__global__ void untile_rec_kernel(BaUntile u, int64_t cnt) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= cnt) return;
+  const int64_t bt = u.tile0 + t;
+  const HimuonParamDesc& P = u.params[find_param(u.params, u.n_params, bt)];
+  const int64_t lt = bt - P.tile0;
+  const int64_t v[6] = {(int64_t)(uintptr_t)P.update, P.ld_upd, P.h, P.w, (lt / P.C) * u.tile_h, (lt % P.C) * u.tile_w};
+  int32_t* r = u.rec + t * kRecInts;
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    r[2 * k] = (int32_t)(uint32_t)(uint64_t)v[k];
+    r[2 * k + 1] = (int32_t)(uint32_t)((uint64_t)v[k] >> 32);
+  }
+  r[12] = __float_as_int(P.upd_scale);
+  r[13] = P.group;
+  r[14] = r[15] = 0;
+}
+
+struct UParam {
+  void* base;        // the parameter (its descriptor's `update`)
+  int64_t h, w, ld;  // shape and row stride
+  int64_t r0, c0;    // parameter row and column of the tile's element (0, 0)
+  float sc;          // upd_scale
+  float s, alpha;    // the group's (1 - lr wd, -lr)
+};
+
+// A tile's record (lane k < 16 holds int k, loaded at the item's start) and
+// the (scale, alpha) table (lane k holds float k) as wave-uniform values.
+HM_DEV UParam uparam_get(int recv, float sav) {
+  auto rd = [&](int k) { return (uint32_t)__builtin_amdgcn_readlane(recv, k); };
+  auto i64 = [&](int k) { return (int64_t)(((uint64_t)rd(k + 1) << 32) | rd(k)); };
+  UParam p;
+  p.base = (void*)(uintptr_t)i64(0);
+  p.ld = i64(2);
+  p.h = i64(4);
+  p.w = i64(6);
+  p.r0 = i64(8);
+  p.c0 = i64(10);
+  p.sc = __uint_as_float(rd(12));
+  const int group = (int)rd(13);
+  p.s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sav), 2 * group));
+  p.alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sav), 2 * group + 1));
+  return p;
+}
+
+// Parameter accesses of the fused untile go through global-address-space
+// pointers: as flat accesses (what a pointer read from a record becomes) they
+// would also count in lgkmcnt, and every LDS wait of the epilogue would then
+// wait for the parameter loads and stores in flight.
+typedef __attribute__((address_space(1))) u32x4_t g_u32x4;
+typedef __attribute__((address_space(1))) uint16_t g_u16;
+typedef __attribute__((address_space(1))) float g_f32;
+
+// One 32-row block of X' as the untile with WD/LR of himuon_untile_apply
+// applies it (elem_ops.h put8 / wdlr8 / wdlr_elems): lane rows[n] holds tile
+// row i + 8 n, columns j .. j + 7 (bf16); u = upd_scale X' (fp32), and
+// p = rd(fma(alpha, rd(u), rd(p s))) for every element inside the tile and the
+// parameter. Whole 8-element vectors load their parameter values first (all
+// 4 rows, 2 at a time for fp32 parameters); others go one element at a time.
+// u = upd_scale X' for the 8 bf16 values of x.
+HM_DEV void ba_updates(const u32x4_t x, float sc, float (&y)[8]) {
+#pragma unroll
+  for (int w2 = 0; w2 < 4; ++w2) {
+    y[2 * w2] = sc * __uint_as_float(x[w2] << 16);
+    y[2 * w2 + 1] = sc * __uint_as_float(x[w2] & 0xffff0000u);
+  }
+}
+
+// 8 parameter values as load8<DT> reads them, from their raw bytes.
+template <int DT>
+HM_DEV void ba_unpack(const u32x4_t (&raw)[DT == HIMUON_DTYPE_F32 ? 2 : 1], float (&p)[8]) {
+#pragma unroll
+  for (int w2 = 0; w2 < 4; ++w2) {
+    if constexpr (DT == HIMUON_DTYPE_F32) {
+      p[w2] = __uint_as_float(raw[0][w2]);
+      p[4 + w2] = __uint_as_float(raw[1][w2]);
+    } else {
+      p[2 * w2] = bf16_to_f32(raw[0][w2] & 0xffffu);
+      p[2 * w2 + 1] = __uint_as_float(raw[0][w2] & 0xffff0000u);
+    }
+  }
+}
+
+// 8 parameter values stored as store8<DT> stores them.
+template <int DT>
+HM_DEV void ba_store(g_u32x4* dst, const float (&p)[8]) {
+  if constexpr (DT == HIMUON_DTYPE_F32) {
+    dst[0] = u32x4_t{__float_as_uint(p[0]), __float_as_uint(p[1]), __float_as_uint(p[2]), __float_as_uint(p[3])};
+    dst[1] = u32x4_t{__float_as_uint(p[4]), __float_as_uint(p[5]), __float_as_uint(p[6]), __float_as_uint(p[7])};
+  } else {
+    u32x4_t w;
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2) w[w2] = pack2(f32_to_bf16(p[2 * w2]), f32_to_bf16(p[2 * w2 + 1]));
+    dst[0] = w;
+  }
+}
+
+template <int DT>
+HM_DEV void ba_untile_block(const UParam& up, const BaUntile& u, const u32x4_t (&rows)[4], int i, int j) {
+#pragma clang fp contract(off)
+  static_assert(DT == HIMUON_DTYPE_F32 || DT == HIMUON_DTYPE_BF16, "fp32 or bf16 parameters");
+  constexpr bool F32 = DT == HIMUON_DTYPE_F32;
+  constexpr int ES = F32 ? 4 : 2, NQ = F32 ? 2 : 1;
+  const int64_t pc = up.c0 + j;
+  const bool col_ok = j < u.tile_w && pc < up.w;
+  const bool col_full = j + 8 <= u.tile_w && pc + 8 <= up.w;
+  char* const base = static_cast<char*>(up.base);
+  const int64_t ou0 = (up.r0 + i) * up.ld + pc;  // row i's first element
+  // The common case, decided per wave (no divergent branch, so the compiler
+  // counts the loads in flight exactly instead of waiting for all of them):
+  // every lane's 4 rows are whole, 16-byte aligned 8-element vectors.
+  const bool all_full = col_full && i + 24 < u.tile_h && up.r0 + i + 24 < up.h &&
+                        aligned16<DT>(up.base, ou0) && ((up.ld * ES) & 15) == 0;
+  if (__all(all_full)) {
+    constexpr int NB = F32 ? 2 : 4;  // rows whose loads are in flight together
+#pragma unroll
+    for (int n0 = 0; n0 < 4; n0 += NB) {
+      u32x4_t raw[NB][NQ];
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        const g_u32x4* src = (const g_u32x4*)(base + (ou0 + 8 * (n0 + k) * up.ld) * ES);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) raw[k][q] = src[q];
+      }
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        float y[8], p[8];
+        ba_updates(rows[n0 + k], up.sc, y);
+        ba_unpack<DT>(raw[k], p);
+        wdlr8<DT>(p, y, up.s, up.alpha);
+        ba_store<DT>((g_u32x4*)(base + (ou0 + 8 * (n0 + k) * up.ld) * ES), p);
+      }
+    }
+    return;
+  }
+  // Edge tiles, ragged or unaligned parameters: element by element inside
+  // the tile and the parameter, as wdlr_elems<DT> (static indices).
+  const int valid = col_ok ? (int)min<int64_t>(min(8, u.tile_w - j), up.w - pc) : 0;
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int ii = i + 8 * n;
+    const int64_t pr = up.r0 + ii;
+    const int nv = (ii < u.tile_h && pr < up.h) ? valid : 0;
+    if (nv == 0) continue;
+    const int64_t ou = pr * up.ld + pc;
+    float y[8];
+    ba_updates(rows[n], up.sc, y);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (e < nv) {
+        if constexpr (F32) {
+          g_f32* q = (g_f32*)(base + (ou + e) * ES);
+          const float p1 = round_to<DT>(*q * up.s);
+          *q = __builtin_fmaf(up.alpha, round_to<DT>(y[e]), p1);
+        } else {
+          g_u16* q = (g_u16*)(base + (ou + e) * ES);
+          const float p1 = round_to<DT>(bf16_to_f32(*q) * up.s);
+          *q = (uint16_t)f32_to_bf16(__builtin_fmaf(up.alpha, round_to<DT>(y[e]), p1));
+        }
+      }
+    }
+  }
+}
+
 // One ring unit: 4 x 16 bytes per lane (32 rows x 64 columns per wave).
 struct Unit {
   u32x4_t v[4];
@@ -142,9 +317,12 @@ constexpr int E2_VMEM_AFTER_DMA = 3 * 4 + (AHEAD - 1) * 4;
 static_assert(E2_VMEM_AFTER_DMA < 64, "vmcnt range");
 
 // SC (the first iteration): every X value (stage-2 rows, the a X term) is
-// replaced by bf16(x xinv[tile]) before it is used.
-template <bool ROUND_ONCE, bool SC>
+// replaced by bf16(x xinv[tile]) before it is used. UDT >= 0 (the last
+// iteration of himuon_ns5_untile_apply, not SC): X' is not stored; the
+// untile with WD/LR applies it to the parameters (dtype UDT) of g.u.
+template <bool ROUND_ONCE, bool SC, int UDT = -1>
 __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
+  static_assert(UDT < 0 || !SC, "the fused untile runs in a last iteration that is not the first");
   __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[LDS_BYTES];
   lds_u8* const lds = (lds_u8*)lds_raw;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -246,6 +424,16 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     const int ni0 = P * (next & 3);
     float xs = 1.f;
     if constexpr (SC) xs = uniform_load_f32(g.xinv, tile);
+    // fused untile: the tile's record and the (scale, alpha) table, one int
+    // or float per lane, first used in the stage-2 epilogue
+    int urec = 0;
+    float usa = 0.f;
+    if constexpr (UDT >= 0) {
+      typedef __attribute__((address_space(1))) const int32_t g_ci32;
+      typedef __attribute__((address_space(1))) const float g_cf32;
+      urec = lane < kRecInts ? ((g_ci32*)g.u.rec)[tile * kRecInts + lane] : 0;
+      usa = ((g_cf32*)g.u.sa)[lane];
+    }
 
     f32x16_t acc[2][4];
 #pragma unroll
@@ -387,6 +575,8 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     // X_P unit q (rows 32 q ..) sits in ring[(2 NUNIT + q) % NSLOT] = ring[q],
     // in the row layout of the stores (row 8 n + l / 8, columns 8 (l % 8) ..).
     const int el32 = lane_o & 31, ehi = lane_o >> 5, erow = lane_o >> 3, ech = lane_o & 7;
+    UParam up;
+    if constexpr (UDT >= 0) up = uparam_get(urec, usa);
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       if (ti == 1 && more) {
@@ -455,8 +645,12 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
 #pragma unroll
         for (int n = 0; n < 4; ++n) rows[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
       }
+      if constexpr (UDT >= 0) {
+        ba_untile_block<UDT>(up, g.u, rows, i0 + 32 * ti + erow, col0 + 8 * ech);
+      } else {
 #pragma unroll
-      for (int n = 0; n < 4; ++n) gstore16(Yt + (i0 + 32 * ti + 8 * n) * T, xl_o, rows[n]);
+        for (int n = 0; n < 4; ++n) gstore16(Yt + (i0 + 32 * ti + 8 * n) * T, xl_o, rows[n]);
+      }
       // the next item's stage-1 units 0..2 into the slots X_P units 0..2 freed
       if (more && ti < AHEAD) load_rows(nAt, 32 * ti, ring[ti]);
     }
@@ -484,14 +678,30 @@ int num_cus() {
 bool ns5_ba_supported(int mp, int np) { return mp == T && np == T; }
 
 bool ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, const float* xinv, int64_t cnt, float a,
-                float b, float c, bool round_once, hipStream_t s) {
+                float b, float c, bool round_once, hipStream_t s, const BaUntile* untile) {
   static_assert(kBaMaxTiles * (T / P) < (int64_t(1) << 31), "32-bit work-item indices");
   if (cnt < 1 || cnt > kBaMaxTiles) return false;
   const int64_t items = cnt * (T / P);
   const int64_t per_xcd = (items + 7) / 8;
   const int64_t wgs_per_xcd = std::max<int64_t>(1, std::min<int64_t>(num_cus() / 8, per_xcd));
-  const BaArgs args{A, X, Y, cnt, a, b, c, round_once ? 1 : 0, xinv};
+  const BaArgs args{A, X, Y, cnt, a, b, c, round_once ? 1 : 0, xinv, untile ? *untile : BaUntile{}};
   const dim3 grid((unsigned)(8 * wgs_per_xcd));
+  if (untile) {
+    if (xinv || !untile->params || untile->n_params <= 0 || !untile->sa || !untile->rec) return false;
+    hipLaunchKernelGGL(untile_rec_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s, *untile, cnt);
+#define HM_BA_UNTILE(DT)                                                                      \
+  if (round_once)                                                                            \
+    hipLaunchKernelGGL((ns_ba_kernel<true, false, DT>), grid, dim3(NTH), 0, s, args);        \
+  else                                                                                       \
+    hipLaunchKernelGGL((ns_ba_kernel<false, false, DT>), grid, dim3(NTH), 0, s, args);
+    switch (untile->param_dtype) {
+      case HIMUON_DTYPE_F32: HM_BA_UNTILE(HIMUON_DTYPE_F32); break;
+      case HIMUON_DTYPE_BF16: HM_BA_UNTILE(HIMUON_DTYPE_BF16); break;
+      default: return false;  // fp16 parameters take the separate untile
+    }
+#undef HM_BA_UNTILE
+    return true;
+  }
   if (round_once && xinv)
     hipLaunchKernelGGL((ns_ba_kernel<true, true>), grid, dim3(NTH), 0, s, args);
   else if (round_once)

@@ -153,6 +153,21 @@ HM_DEV u32x2_t quad_transpose(u32x2_t w, int k) {
 }
 
 
+// The untile with WD/LR fused into the last NS iteration of 512 x 512 tiles
+// (himuon_ns5_untile_apply): instead of storing X', the fused kernel's
+// epilogue applies each value u = upd_scale X' of tile tile0 + t (t the tile's
+// index in the launch) to its parameter element in place, as
+// himuon_untile_apply does (tiles not transposed: tile_h <= tile_w).
+struct BaUntile {
+  const HimuonParamDesc* params;  // device descriptor table of the bucket
+  int n_params;
+  int64_t tile0;                  // bucket tile index of the launch's tile 0
+  int tile_h, tile_w;
+  int param_dtype;
+  const float* sa;                // device (scale, alpha) per param group, 2 x HIMUON_APPLY_MAX_GROUPS floats
+  int32_t* rec;                   // device scratch of 16 int32 per tile of the launch (set by ns5_stream_run)
+};
+
 // Persistent streamed-operand 256-block path (ns5_stream.hip): mp, np
 // multiples of 256. Runs `steps` iterations on `cnt` tiles from the raw x
 // (the first iteration scales X0 = bf16(x inv) on load), ping-ponging X
@@ -162,9 +177,11 @@ HM_DEV u32x2_t quad_transpose(u32x2_t w, int k) {
 // mp == np == 512), wsB unused. Returns 0, or HIMUON_EINVAL (nothing
 // launched) when cnt is too large for the fused kernel.
 bool ns5_stream_supported(int mp, int np);
+// untile (fused_ba only; steps >= 2): the last iteration applies the untile
+// with WD/LR instead of storing its result.
 int ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
                     float a, float b, float c, bool round_once, bool fused_ba, uint16_t* wsA, uint16_t* wsB,
-                    hipStream_t s);
+                    hipStream_t s, const BaUntile* untile = nullptr);
 
 // Fused B = bf16(c A A^T + b A), Y = bf16(bf16(B X) + a X) (ns5_ba.hip) on
 // `cnt` 512 x 512 tiles: A from the first product, X -> Y (Y != X). xinv
@@ -174,8 +191,10 @@ int ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int 
 // launched and false returned.
 constexpr int64_t kBaMaxTiles = (int64_t(1) << 29) - 1;
 bool ns5_ba_supported(int mp, int np);
+// untile non-null: Y is not written; the results update the parameters
+// (xinv must be null, param_dtype fp32 or bf16; false otherwise).
 bool ns5_ba_run(const uint16_t* A, const uint16_t* X, uint16_t* Y, const float* xinv, int64_t cnt, float a,
-                float b, float c, bool round_once, hipStream_t s);
+                float b, float c, bool round_once, hipStream_t s, const BaUntile* untile = nullptr);
 
 // One NS product over `ntiles` batch entries on the 256-block stream kernels
 // (M, N, K multiples of 256; row pitches in elements, batch strides):

@@ -614,8 +614,9 @@ void ns_stream_product(int mode, const uint16_t* P, int64_t p_bs, int ldp, const
 // (X0 is never written); A and B live in the workspace.
 int ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int mp, int np, int steps,
                    float a, float b, float c, bool round_once, bool fused_ba, uint16_t* wsA, uint16_t* wsB,
-                   hipStream_t s) {
+                   hipStream_t s, const BaUntile* untile) {
   if (fused_ba && cnt > kBaMaxTiles) return HIMUON_EINVAL;
+  if (untile && (!fused_ba || steps < 2)) return HIMUON_EINVAL;
   const int64_t sq = (int64_t)mp * mp, rect = (int64_t)mp * np;
   const int nb = mp / BT;
   const int64_t gram_items = cnt * (nb * (nb + 1) / 2);
@@ -630,7 +631,15 @@ int ns5_stream_run(uint16_t* x, uint16_t* y, const float* inv, int64_t cnt, int 
     else
       launch<kGramA>(ga, gram_items, s);
     if (fused_ba) {  // B stays on chip: ns5_ba.hip
-      if (!ns5_ba_run(wsA, cur, nxt, xinv, cnt, a, b, c, round_once, s)) return HIMUON_EINVAL;
+      // the untile fused into the last iteration; its per-tile records go to
+      // wsB, which the fused path does not use otherwise (cnt mp^2 bf16)
+      BaUntile u{};
+      if (untile && it + 1 == steps) {
+        u = *untile;
+        u.rec = reinterpret_cast<int32_t*>(wsB);
+      }
+      if (!ns5_ba_run(wsA, cur, nxt, xinv, cnt, a, b, c, round_once, s, u.params ? &u : nullptr))
+        return HIMUON_EINVAL;
       std::swap(cur, nxt);
       continue;
     }

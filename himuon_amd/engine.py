@@ -215,6 +215,28 @@ class TileGroup:
             workspace, sub_batch, family=self.ns_family, round_once=self.round_once, rows=self.m,
         )
 
+    def ns_untile_ok(self, steps: int) -> bool:
+        """True when the untile with WD/LR can run inside the last NS
+        iteration (himuon_ns5_untile_apply): fused mode, 512 x 512 NS tiles
+        without transpose, family "auto", steps >= 2, fp32 or bf16 parameters."""
+        return self.fused and nat.ns5_untile_apply_supported(
+            self.mp, self.np, self.tile_h, self.tile_w, steps, self.upd_dtype, self.ns_family, self.round_once)
+
+    def ns_untile(self, start: int, count: int, steps: int, workspace: torch.Tensor, sub_batch: int,
+                  scale_alpha: torch.Tensor) -> None:
+        """NS of tiles start .. start + count - 1 with the untile and the WD/LR
+        of scale_alpha fused into the last iteration (the parameters of those
+        tiles are updated; untile() must not run for them afterwards)."""
+        if count <= 0:
+            return
+        r = self._rng
+        nat.ns5_untile_apply(
+            r(self.tiles, start, count), r(self.alt, start, count), self.inv[start : start + count], count,
+            self.mp, self.np, steps, workspace, sub_batch, self.desc, len(self.tile0), start, self.tile_h,
+            self.tile_w, self.upd_dtype, scale_alpha, family=self.ns_family, round_once=self.round_once,
+            rows=self.m,
+        )
+
     def lds_step_ok(self) -> bool:
         """True when the whole step of this group runs as one launch per chunk
         (himuon_lds_step): fused mode, 128 x 128 NS tiles without transpose,

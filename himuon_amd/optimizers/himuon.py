@@ -69,6 +69,9 @@ class HiMuon(Optimizer):
     # WD/LR) as one LDS-resident launch per chunk (himuon_lds_step); False
     # keeps the gather / NS / untile launches (same results, bit for bit).
     _fuse_lds_step: bool = True
+    # fused-untile buckets of 512 x 512 tiles: the untile with WD/LR runs
+    # inside the last NS iteration (himuon_ns5_untile_apply)
+    _fuse_ns_untile: bool = True
     # NS kernel family of every tile group (a key of _native.NS_FAMILIES):
     # "auto", the per-geometry choice; the others are comparison runs, which
     # also keep 128 x 128 buckets off the one-launch LDS step for "block128".
@@ -743,6 +746,7 @@ class HiMuon(Optimizer):
         for g in groups:
             grp: TileGroup = g["tiles"]
             lds = self._fuse_lds_step and grp.lds_step_ok()
+            nsu = not lds and self._fuse_ns_untile and grp.ns_untile_ok(g["steps"])
             if not lds:
                 grp.gather()
             ofs = 0
@@ -753,6 +757,8 @@ class HiMuon(Optimizer):
                     ev0.record()
                 if lds:
                     grp.lds_step(ofs, c, g["steps"], self._lrwd)
+                elif nsu:
+                    grp.ns_untile(ofs, c, g["steps"], self._workspace, g["sub_batch"], self._lrwd)
                 else:
                     grp.ns(ofs, c, g["steps"], self._workspace, g["sub_batch"])
                 if use_events:
@@ -763,10 +769,10 @@ class HiMuon(Optimizer):
                 ofs += c
             if grp.fused:
                 # WD/LR applied by the untile itself (or by the LDS-resident
-                # step), from the (scale, alpha) table written before this
-                # step; the graph path still lists the parameters as pending
-                # (without an update tensor).
-                if not lds:
+                # step, or inside the last NS iteration), from the (scale,
+                # alpha) table written before this step; the graph path still
+                # lists the parameters as pending (without an update tensor).
+                if not (lds or nsu):
                     grp.untile(g["steps"], self._lrwd)
                 if self._in_graph_region:
                     for (p, _), gi in zip(g["entries"], g["group_idx"]):

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HIMUON_ABI_VERSION 4
+#define HIMUON_ABI_VERSION 5
 
 /* Element type codes for gradients / momentum / updates. */
 #define HIMUON_DTYPE_F32 0
@@ -332,6 +332,29 @@ int himuon_untile_apply(const HimuonParamDesc* params_dev, int n_params,
                         int64_t n_tiles, int tile_h, int tile_w, int mp, int np,
                         int param_dtype, const uint16_t* tiles_bf16,
                         const float* scale_alpha_dev, void* stream);
+
+/*
+ * NS5 with the untile with WD/LR fused into its last iteration: the same
+ * result as himuon_ns5_ex on tiles x / y followed by himuon_untile_apply of
+ * that result, for the bucket tiles tile_begin .. tile_begin + n_tiles - 1 of
+ * the descriptor table (x = the bucket's tile buffer advanced to tile
+ * tile_begin; the untile's tile numbering is the bucket's). The last
+ * iteration's kernel applies each value to its parameter as it computes it
+ * instead of writing the NS result, so x and y hold no result afterwards.
+ * Supported (else HIMUON_EINVAL, nothing launched; the caller runs the two
+ * calls instead) for 512 x 512 NS tiles (mp == np == 512) that are not
+ * transposed (tile_h <= tile_w), family AUTO, steps >= 2 and fp32 or bf16
+ * parameters; himuon_ns5_untile_apply_supported answers for a geometry.
+ * Replaces newton_schulz + _post_ns_per_param + the Muon parameters'
+ * outside-graph WD/LR of one chunk (himuon.py:232-284, 315-348, 215-228).
+ */
+int himuon_ns5_untile_apply_supported(int mp, int np, int tile_h, int tile_w, int steps, int flags,
+                                      int param_dtype);
+int himuon_ns5_untile_apply(uint16_t* x, uint16_t* y, const float* inv, int64_t n_tiles, int mp, int np,
+                            int steps, float a, float b, float c, void* workspace, size_t workspace_bytes,
+                            int64_t sub_batch, int flags, const HimuonParamDesc* params_dev, int n_params,
+                            int64_t tile_begin, int tile_h, int tile_w, int param_dtype,
+                            const float* scale_alpha_dev, void* stream);
 
 /*
  * Write the table himuon_untile_apply reads: scale_alpha_dev[2 g] =

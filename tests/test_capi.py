@@ -193,6 +193,23 @@ def test_ns5_ex_and_stage_argument_errors(lib):
     for bad in (dict(th=256), dict(tw=256), dict(th=100, tw=64), dict(dt=2), dict(pdt=2), dict(steps=-1),
                 dict(flags=1), dict(prm=z), dict(npar=0), dict(sa=z), dict(base=-1), dict(n=-1), dict(th=0)):
         assert lds(**bad) == -22, bad
+    # NS with the untile fused into its last iteration: 512 x 512 NS tiles, not
+    # transposed, family AUTO (the 2-D rounding allowed), steps >= 2, fp32/bf16
+    # parameters, a descriptor table and a (scale, alpha) table
+    sup = lib.himuon_ns5_untile_apply_supported
+    assert sup(512, 512, 512, 512, 5, 0, 1) and sup(512, 512, 300, 500, 2, 0x10, 0)
+    for args in ((256, 512, 256, 512, 5, 0, 1), (512, 1024, 512, 1024, 5, 0, 1), (512, 512, 500, 300, 5, 0, 1),
+                 (512, 512, 512, 512, 1, 0, 1), (512, 512, 512, 512, 5, 1, 1), (512, 512, 512, 512, 5, 2, 1),
+                 (512, 512, 512, 512, 5, 0, 2), (512, 512, 600, 600, 5, 0, 1), (512, 512, 0, 512, 5, 0, 1)):
+        assert not sup(*args), args
+
+    def nsu(n=0, mp=512, np_=512, steps=5, flags=0, prm=8, npar=2, base=0, th=512, tw=512, pdt=1, sa=16):
+        return lib.himuon_ns5_untile_apply(8, 16, 24, n, mp, np_, steps, 1.0, 1.0, 1.0, 32, 1 << 30, 4, flags, prm,
+                                           npar, base, th, tw, pdt, sa, z)
+    assert nsu() == 0 and nsu(flags=0x10, th=400, pdt=0) == 0  # empty work: no launch
+    for bad in (dict(mp=256), dict(steps=1), dict(flags=1), dict(th=513), dict(pdt=2), dict(prm=z), dict(npar=0),
+                dict(base=-1), dict(sa=z), dict(th=512, tw=500)):
+        assert nsu(**bad) == -22, bad
 
 
 def test_geometry_helpers():

@@ -9,19 +9,23 @@ and checks, with the grads copied to the host where the oracle needs them:
 * momentum buffers of whole sampled matrices bit-exact against
   oracle.momentum applied once per step (the grads stay in place, as a
   training loop with zero_grad(set_to_none=False) keeps them);
-* NS tiles sampled across every sub-batch, including tiles whose offset in
-  the tile buffer is past 4 GiB, against the reference's NS5 in the same
+* tiles sampled across every sub-batch, including tiles whose offset in the
+  tile buffer is past 4 GiB: where the bucket stores its NS result (cfg3's
+  full-matrix groups), the NS tiles against the reference's NS5 in the same
   dtypes (torch on the GPU, ns5_torch_staged): the north star's per-tile
-  relative Frobenius error <= 1e-2, and bit-identical as built;
-* the singular values of sampled tiles against the quintic's band;
-* every NS output finite;
+  relative Frobenius error <= 1e-2 and bit-identical as built, their singular
+  values against the quintic's band, every NS output finite;
 * the parameters of the sampled tiles after the last replay bit-exact against
-  oracle.apply_update of the sampled NS tile (WD/LR fused in the untile).
+  oracle.apply_update of the sampled NS tile, or of torch's NS5 of the same
+  inputs where no NS result is stored (WD/LR fused in the untile).
 
-cfg5's 128 x 128-tile bucket runs the whole step in LDS (himuon_lds_step) and
-stores no NS result: its check is the parameters of the sampled tiles against
+cfg5's 128 x 128-tile bucket runs the whole step in LDS (himuon_lds_step), and
+the 512 x 512-tile buckets (cfg2, cfg4, cfg5 after reconfigure) apply the untile
+with WD/LR inside the last NS iteration (himuon_ns5_untile_apply): neither stores
+an NS result, so their check is the parameters of the sampled tiles against
 oracle.apply_update of torch's NS5 of the same inputs (tests/test_gpu_lds_step.py
-pins that kernel bit for bit against the separate launches).
+and tests/test_gpu_ns_untile.py pin those kernels bit for bit against the
+separate launches, whose NS tiles tests/test_gpu_kernels.py checks).
 
 Full-matrix groups (cfg3) compare against the 2-D third product of the
 reference (torch.addmm, himuon.py:249-253). cfg5 runs the tile-128 regime,
@@ -85,9 +89,11 @@ def _check_group(opt, gi, sample, n_steps, p_before, round_once=False, label="")
     same-dtype NS5, momentum region bit-exact, band, fused-untile parameters."""
     g = opt._groups[gi]
     grp = g["tiles"]
-    # 128 x 128-tile buckets run the whole step in LDS (himuon_lds_step): no
-    # NS result is stored, the parameters are the output checked
-    no_tiles = opt._fuse_lds_step and grp.lds_step_ok()
+    # 128 x 128-tile buckets run the whole step in LDS (himuon_lds_step), and
+    # 512 x 512-tile buckets apply the untile inside the last NS iteration
+    # (himuon_ns5_untile_apply): no NS result is stored, the parameters are
+    # the output checked
+    no_tiles = (opt._fuse_lds_step and grp.lds_step_ok()) or (opt._fuse_ns_untile and grp.ns_untile_ok(g["steps"]))
     res = None if no_tiles else grp.result(g["steps"])
     if not no_tiles:
         assert torch.isfinite(res.float()).all(), f"{label}: non-finite NS output"
@@ -107,7 +113,8 @@ def _check_group(opt, gi, sample, n_steps, p_before, round_once=False, label="")
     X = torch.stack(inputs).to("cuda")
     ref = ns5_torch_staged(X, steps=g["steps"], round_once=round_once)
     if no_tiles:
-        print(f"  {label}: step in LDS: {len(sample)} tiles' parameters vs torch NS5 + oracle WD/LR", flush=True)
+        print(f"  {label}: NS result not stored: {len(sample)} tiles' parameters vs torch NS5 + oracle WD/LR",
+              flush=True)
         assert torch.isfinite(ref).all()
         _check_params(grp, sample, ref.float(), p_before, label)
         return
