@@ -324,6 +324,49 @@ def kernel_roofline(config: str, dk: dict) -> dict:
     return out
 
 
+def time_ns_untile_stage(opt, reps: int) -> float | None:
+    """Average ms of NS5 + untile (with WD/LR) as the step runs them: one
+    launch per chunk where the untile is fused into the last NS iteration,
+    else the NS launches and then the untile. HIP events on the launch
+    stream; each rep re-gathers first (untimed). None when no group takes
+    the fused path (ns5_ms + untile_ms then cover the same work)."""
+    groups = [g for g in opt._groups
+              if not (opt._fuse_lds_step and g["tiles"].lds_step_ok())]
+    if not any(opt._fuse_ns_untile and g["tiles"].ns_untile_ok(g["steps"]) for g in groups):
+        return None
+    s = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+
+    def run():
+        for g in groups:
+            grp = g["tiles"]
+            nsu = opt._fuse_ns_untile and grp.ns_untile_ok(g["steps"])
+            ofs = 0
+            for c in g["chunks"]:
+                if nsu:
+                    grp.ns_untile(ofs, c, g["steps"], opt._workspace, g["sub_batch"], opt._lrwd)
+                else:
+                    grp.ns(ofs, c, g["steps"], opt._workspace, g["sub_batch"])
+                ofs += c
+            if not nsu and grp.fused:
+                grp.untile(g["steps"], opt._lrwd)
+            elif not nsu:
+                grp.untile(g["steps"])
+
+    for g in groups:
+        g["tiles"].gather()
+    run()
+    torch.cuda.synchronize()
+    for e0, e1 in evs:
+        for g in groups:
+            g["tiles"].gather()
+        e0.record(s)
+        run()
+        e1.record(s)
+    torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in evs) / reps
+
+
 def time_io_stage(opt, reps: int) -> tuple[float, float]:
     """Average ms of gather (+normaliser) and of untile for one step (for a
     fused group, the untile that applies WD/LR to the parameters in place)."""
@@ -968,6 +1011,7 @@ def main():
     ns_ms = time_ns_stage(opt, reps=max(3, args.steps // 2))
     dk = time_dominant_kernel(opt, reps=max(3, args.steps // 2))
     gather_ms, untile_ms = time_io_stage(opt, reps=max(3, args.steps // 2))
+    nsu_ms = time_ns_untile_stage(opt, reps=max(3, args.steps // 2))
     lds_step_ms = time_lds_step_stage(opt, reps=max(3, args.steps // 2))
     apply_ms = time_apply(opt, reps=max(3, args.steps // 2))
     flops = algorithmic_flops(opt)
@@ -1014,6 +1058,10 @@ def main():
         "untile_ms": round(untile_ms, 3),
         "untile_gbs": round(((2 + 2 * pb) if fused else (2 + ub)) * n_el / (untile_ms * 1e-3) / 1e9, 1),
         "untile_applies_wd_lr": fused,
+        # NS5 + untile as the step runs them, the untile fused into the last
+        # NS iteration of 512 x 512 buckets (ns5_ms and untile_ms above time
+        # the two launches that this replaces)
+        "ns5_untile_fused_ms": None if nsu_ms is None else round(nsu_ms, 3),
         # 128 x 128-tile buckets run the whole step as one LDS-resident launch
         # per chunk; ns5/gather/untile above then time the launches it replaces
         "lds_step_ms": None if lds_step_ms is None else round(lds_step_ms, 3),

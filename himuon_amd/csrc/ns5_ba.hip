@@ -229,8 +229,11 @@ HM_DEV void ba_store(g_u32x4* dst, const float (&p)[8]) {
   }
 }
 
+// Returns whether the block took the whole-vector path (wave-uniform): its
+// VMEM instructions are then 4 NQ loads and 4 NQ stores; on the element path
+// their number depends on the data and may be zero.
 template <int DT>
-HM_DEV void ba_untile_block(const UParam& up, const BaUntile& u, const u32x4_t (&rows)[4], int i, int j) {
+HM_DEV bool ba_untile_block(const UParam& up, const BaUntile& u, const u32x4_t (&rows)[4], int i, int j) {
 #pragma clang fp contract(off)
   static_assert(DT == HIMUON_DTYPE_F32 || DT == HIMUON_DTYPE_BF16, "fp32 or bf16 parameters");
   constexpr bool F32 = DT == HIMUON_DTYPE_F32;
@@ -265,7 +268,7 @@ HM_DEV void ba_untile_block(const UParam& up, const BaUntile& u, const u32x4_t (
         ba_store<DT>((g_u32x4*)(base + (ou0 + 8 * (n0 + k) * up.ld) * ES), p);
       }
     }
-    return;
+    return true;
   }
   // Edge tiles, ragged or unaligned parameters: element by element inside
   // the tile and the parameter, as wdlr_elems<DT> (static indices).
@@ -294,6 +297,7 @@ HM_DEV void ba_untile_block(const UParam& up, const BaUntile& u, const u32x4_t (
       }
     }
   }
+  return false;
 }
 
 // One ring unit: 4 x 16 bytes per lane (32 rows x 64 columns per wave).
@@ -576,6 +580,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     // in the row layout of the stores (row 8 n + l / 8, columns 8 (l % 8) ..).
     const int el32 = lane_o & 31, ehi = lane_o >> 5, erow = lane_o >> 3, ech = lane_o & 7;
     UParam up;
+    bool ufast = true;  // fused untile: blocks 1-3 all took the whole-vector path
     if constexpr (UDT >= 0) up = uparam_get(urec, usa);
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
@@ -646,7 +651,8 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
         for (int n = 0; n < 4; ++n) rows[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
       }
       if constexpr (UDT >= 0) {
-        ba_untile_block<UDT>(up, g.u, rows, i0 + 32 * ti + erow, col0 + 8 * ech);
+        const bool f = ba_untile_block<UDT>(up, g.u, rows, i0 + 32 * ti + erow, col0 + 8 * ech);
+        if (ti >= 1) ufast = ufast && f;
       } else {
 #pragma unroll
         for (int n = 0; n < 4; ++n) gstore16(Yt + (i0 + 32 * ti + 8 * n) * T, xl_o, rows[n]);
@@ -656,8 +662,14 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     }
     if (!more) break;
     // this group's half of the next A_P landed (issued before the
-    // E2_VMEM_AFTER_DMA stores and loads above)
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(E2_VMEM_AFTER_DMA) : "memory");
+    // E2_VMEM_AFTER_DMA stores and loads above). With the fused untile, a
+    // block on the element path may issue fewer than the 4 stores counted
+    // (none at all outside the parameter): then only the ring loads are
+    // certain to be younger than the direct-to-LDS loads.
+    if (UDT < 0 || ufast)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(E2_VMEM_AFTER_DMA) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"((AHEAD - 1) * 4) : "memory");
     lds_barrier();
     item = next;
   }
