@@ -229,15 +229,21 @@ HM_DEV void ba_store(g_u32x4* dst, const float (&p)[8]) {
   }
 }
 
-// Returns whether the block took the whole-vector path (wave-uniform): its
-// VMEM instructions are then 4 NQ loads and 4 NQ stores; on the element path
-// their number depends on the data and may be zero.
-template <int DT>
-HM_DEV bool ba_untile_block(const UParam& up, const BaUntile& u, const u32x4_t (&rows)[4], int i, int j) {
+// make_rows(rows) produces the block's X' rows (its LDS staging); EARLY: the
+// whole-vector path issues its first parameter loads before calling it, so
+// that their latency overlaps the staging (the loads' registers are then
+// live beside the staging's). Returns whether the block took the
+// whole-vector path (wave-uniform): its VMEM instructions are then 4 NQ loads
+// and 4 NQ stores; on the element path their number depends on the data and
+// may be zero.
+template <int DT, bool EARLY, typename MakeRows>
+HM_DEV bool ba_untile_block(const UParam& up, const BaUntile& u, MakeRows&& make_rows, int i, int j) {
 #pragma clang fp contract(off)
   static_assert(DT == HIMUON_DTYPE_F32 || DT == HIMUON_DTYPE_BF16, "fp32 or bf16 parameters");
   constexpr bool F32 = DT == HIMUON_DTYPE_F32;
   constexpr int ES = F32 ? 4 : 2, NQ = F32 ? 2 : 1;
+  u32x4_t rows[4];
+  if constexpr (!EARLY) make_rows(rows);
   const int64_t pc = up.c0 + j;
   const bool col_ok = j < u.tile_w && pc < up.w;
   const bool col_full = j + 8 <= u.tile_w && pc + 8 <= up.w;
@@ -259,6 +265,7 @@ HM_DEV bool ba_untile_block(const UParam& up, const BaUntile& u, const u32x4_t (
 #pragma unroll
         for (int q = 0; q < NQ; ++q) raw[k][q] = src[q];
       }
+      if (EARLY && n0 == 0) make_rows(rows);
 #pragma unroll
       for (int k = 0; k < NB; ++k) {
         float y[8], p[8];
@@ -272,6 +279,7 @@ HM_DEV bool ba_untile_block(const UParam& up, const BaUntile& u, const u32x4_t (
   }
   // Edge tiles, ragged or unaligned parameters: element by element inside
   // the tile and the parameter, as wdlr_elems<DT> (static indices).
+  if constexpr (EARLY) make_rows(rows);
   const int valid = col_ok ? (int)min<int64_t>(min(8, u.tile_w - j), up.w - pc) : 0;
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
@@ -595,7 +603,8 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
         dma_half(nAt, ni0, grp, lane_o, cw_o);
       }
       const Unit& xp = ring[(2 * NUNIT + ti) % NSLOT];
-      u32x4_t rows[4];
+      // the block's 32 result rows, in the row layout of the stores
+      auto make_rows = [&](u32x4_t(&rows)[4]) {
       if constexpr (!ROUND_ONCE) {
         // bf16(B X) through W into the row layout, then + a X there with X_P
         // straight from the ring: the same operations on the same values as
@@ -650,10 +659,20 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
 #pragma unroll
         for (int n = 0; n < 4; ++n) rows[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
       }
+      };
       if constexpr (UDT >= 0) {
-        const bool f = ba_untile_block<UDT>(up, g.u, rows, i0 + 32 * ti + erow, col0 + 8 * ech);
+        // block 0's parameter loads after its staging: before it they would
+        // be live beside all of the accumulators (and in the 2-D form, whose
+        // staging holds more registers, every block's)
+        bool f;
+        if (ti == 0 || ROUND_ONCE)
+          f = ba_untile_block<UDT, false>(up, g.u, make_rows, i0 + 32 * ti + erow, col0 + 8 * ech);
+        else
+          f = ba_untile_block<UDT, true>(up, g.u, make_rows, i0 + 32 * ti + erow, col0 + 8 * ech);
         if (ti >= 1) ufast = ufast && f;
       } else {
+        u32x4_t rows[4];
+        make_rows(rows);
 #pragma unroll
         for (int n = 0; n < 4; ++n) gstore16(Yt + (i0 + 32 * ti + 8 * n) * T, xl_o, rows[n]);
       }
