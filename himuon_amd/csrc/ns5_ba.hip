@@ -605,60 +605,60 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
       const Unit& xp = ring[(2 * NUNIT + ti) % NSLOT];
       // the block's 32 result rows, in the row layout of the stores
       auto make_rows = [&](u32x4_t(&rows)[4]) {
-      if constexpr (!ROUND_ONCE) {
-        // bf16(B X) through W into the row layout, then + a X there with X_P
-        // straight from the ring: the same operations on the same values as
-        // in the accumulator layout, without staging X_P
+        if constexpr (!ROUND_ONCE) {
+          // bf16(B X) through W into the row layout, then + a X there with X_P
+          // straight from the ring: the same operations on the same values as
+          // in the accumulator layout, without staging X_P
 #pragma unroll
-        for (int tj = 0; tj < 2; ++tj)
+          for (int tj = 0; tj < 2; ++tj)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f32x16_t& v = acc[tj][ti];
-            *reinterpret_cast<lds_u32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi) =
-                u32x2_t{pk_bf16(v[4 * q], v[4 * q + 1]), pk_bf16(v[4 * q + 2], v[4 * q + 3])};
+            for (int q = 0; q < 4; ++q) {
+              const f32x16_t& v = acc[tj][ti];
+              *reinterpret_cast<lds_u32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi) =
+                  u32x2_t{pk_bf16(v[4 * q], v[4 * q + 1]), pk_bf16(v[4 * q + 2], v[4 * q + 3])};
+            }
+          // all 4 row reads, one wait
+          u32x4_t bxr[4];
+#pragma unroll
+          for (int n = 0; n < 4; ++n) bxr[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
+#pragma unroll
+          for (int n = 0; n < 4; ++n) {
+            const u32x4_t x = SC ? scale8_rne(xp.v[n], xs) : xp.v[n];
+#pragma unroll
+            for (int w2 = 0; w2 < 4; ++w2) {
+              const float y0 = fmaf(ca, __uint_as_float(x[w2] << 16), __uint_as_float(bxr[n][w2] << 16));
+              const float y1 = fmaf(ca, __uint_as_float(x[w2] & 0xffff0000u), __uint_as_float(bxr[n][w2] & 0xffff0000u));
+              rows[n][w2] = pk_bf16(y0, y1);
+            }
           }
-        // all 4 row reads, one wait
-        u32x4_t bxr[4];
+        } else {
+          // bf16(B X + a X): X_P into the accumulator layout through W, the
+          // fp32 sum there, the result back through W into rows
 #pragma unroll
-        for (int n = 0; n < 4; ++n) bxr[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
+          for (int n = 0; n < 4; ++n)
+            *reinterpret_cast<lds_u32x4*>(W + ep_off(8 * n + erow, ech)) = SC ? scale8_rne(xp.v[n], xs) : xp.v[n];
+          // X_P in the accumulator layout: all 8 pieces, one wait
+          u32x2_t xv[2][4];
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          const u32x4_t x = SC ? scale8_rne(xp.v[n], xs) : xp.v[n];
+          for (int tj = 0; tj < 2; ++tj)
 #pragma unroll
-          for (int w2 = 0; w2 < 4; ++w2) {
-            const float y0 = fmaf(ca, __uint_as_float(x[w2] << 16), __uint_as_float(bxr[n][w2] << 16));
-            const float y1 = fmaf(ca, __uint_as_float(x[w2] & 0xffff0000u), __uint_as_float(bxr[n][w2] & 0xffff0000u));
-            rows[n][w2] = pk_bf16(y0, y1);
-          }
+            for (int q = 0; q < 4; ++q)
+              xv[tj][q] = *reinterpret_cast<const lds_cu32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi);
+#pragma unroll
+          for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float y[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                y[e] = fmaf(ca, bf16_to_f32(half16(xv[tj][q][e >> 1], e & 1)), acc[tj][ti][4 * q + e]);
+              *reinterpret_cast<lds_u32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi) =
+                  u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
+            }
+          // the 32 result rows: all 4 row reads, one wait
+#pragma unroll
+          for (int n = 0; n < 4; ++n) rows[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
         }
-      } else {
-        // bf16(B X + a X): X_P into the accumulator layout through W, the
-        // fp32 sum there, the result back through W into rows
-#pragma unroll
-        for (int n = 0; n < 4; ++n)
-          *reinterpret_cast<lds_u32x4*>(W + ep_off(8 * n + erow, ech)) = SC ? scale8_rne(xp.v[n], xs) : xp.v[n];
-        // X_P in the accumulator layout: all 8 pieces, one wait
-        u32x2_t xv[2][4];
-#pragma unroll
-        for (int tj = 0; tj < 2; ++tj)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            xv[tj][q] = *reinterpret_cast<const lds_cu32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi);
-#pragma unroll
-        for (int tj = 0; tj < 2; ++tj)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float y[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              y[e] = fmaf(ca, bf16_to_f32(half16(xv[tj][q][e >> 1], e & 1)), acc[tj][ti][4 * q + e]);
-            *reinterpret_cast<lds_u32x2*>(W + ep_off(el32, 4 * tj + q) + 8 * ehi) =
-                u32x2_t{pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3])};
-          }
-        // the 32 result rows: all 4 row reads, one wait
-#pragma unroll
-        for (int n = 0; n < 4; ++n) rows[n] = *reinterpret_cast<const lds_u32x4*>(W + ep_off(8 * n + erow, ech));
-      }
       };
       if constexpr (UDT >= 0) {
         // block 0's parameter loads after its staging: before it they would
