@@ -1,6 +1,6 @@
 """HiMuon optimizer-step benchmark on one MI355X.
 
-Metric (BASELINE.json): HiMuon step latency (ms) on one MI355X, with NS5
+Metric: HiMuon step latency (ms) on one MI355X, with NS5
 TFLOP/s and its fraction of the bf16 dense MFMA peak.
 
 Default workload: the Qwen3-4B-shaped parameter set (36 layers x {q 4096x2560,

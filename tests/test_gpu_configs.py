@@ -1,4 +1,4 @@
-"""Parity at every BASELINE workload (cfg2-cfg5) on the GPU.
+"""Parity at every benchmark workload (cfg2-cfg5) on the GPU.
 
 Each test builds a config's full parameter set exactly as bench.py does
 (seeded device generator: bf16 or fp32 params, fp32 grads ~N(0, 1e-3^2)),
