@@ -219,13 +219,15 @@ HM_DEV void ba_unpack(const u32x4_t (&raw)[DT == HIMUON_DTYPE_F32 ? 2 : 1], floa
 template <int DT>
 HM_DEV void ba_store(g_u32x4* dst, const float (&p)[8]) {
   if constexpr (DT == HIMUON_DTYPE_F32) {
-    dst[0] = u32x4_t{__float_as_uint(p[0]), __float_as_uint(p[1]), __float_as_uint(p[2]), __float_as_uint(p[3])};
-    dst[1] = u32x4_t{__float_as_uint(p[4]), __float_as_uint(p[5]), __float_as_uint(p[6]), __float_as_uint(p[7])};
+    __builtin_nontemporal_store(
+        u32x4_t{__float_as_uint(p[0]), __float_as_uint(p[1]), __float_as_uint(p[2]), __float_as_uint(p[3])}, dst);
+    __builtin_nontemporal_store(
+        u32x4_t{__float_as_uint(p[4]), __float_as_uint(p[5]), __float_as_uint(p[6]), __float_as_uint(p[7])}, dst + 1);
   } else {
     u32x4_t w;
 #pragma unroll
     for (int w2 = 0; w2 < 4; ++w2) w[w2] = pack2(f32_to_bf16(p[2 * w2]), f32_to_bf16(p[2 * w2 + 1]));
-    dst[0] = w;
+    __builtin_nontemporal_store(w, dst);
   }
 }
 
@@ -263,7 +265,7 @@ HM_DEV bool ba_untile_block(const UParam& up, const BaUntile& u, MakeRows&& make
       for (int k = 0; k < NB; ++k) {
         const g_u32x4* src = (const g_u32x4*)(base + (ou0 + 8 * (n0 + k) * up.ld) * ES);
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) raw[k][q] = src[q];
+        for (int q = 0; q < NQ; ++q) raw[k][q] = __builtin_nontemporal_load(src + q);
       }
       if (EARLY && n0 == 0) make_rows(rows);
 #pragma unroll
