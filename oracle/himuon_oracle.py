@@ -486,7 +486,9 @@ def adamw_step(g, m, v, step, betas, eps, dtype: str = "float32", bias=None):
     t1 = round_to(m / round_to(bc1, dtype), dtype)
     t2 = round_to(np.sqrt(v, dtype=F32), dtype)
     t3 = round_to(round_to(t2 / round_to(sbc2, dtype), dtype) + F32(eps), dtype)
-    u = round_to(t1 / t3, dtype)
+    # (fp16: eps = 1e-8 underflows, so t3 is 0 where v is; x / 0 gives the IEEE inf/NaN torch gives)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        u = round_to(t1 / t3, dtype)
     return u, m, v, s, (bc1, sbc2)
 
 

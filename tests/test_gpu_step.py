@@ -212,7 +212,7 @@ def test_fused_untile_apply_matches_unfused(pdt, cuda_graph, tile):
         for i, (a, r) in enumerate(zip(m.parameters(), ref.parameters())):
             if not torch.equal(a, r):
                 out.append((i, tuple(a.shape), int((a != r).sum()), a.numel(),
-                            float((a.float() - r.float()).abs().max())))
+                            float((a.detach().float() - r.detach().float()).abs().max())))
         return out
 
     if pdt == torch.float16:
