@@ -310,7 +310,7 @@ def test_fp16_params_fp32_grads_eager_matches_graph():
     assert o_g._cuda_graph is not None
     assert not any(grp["tiles"].fused for grp in o_g._groups)
     assert all(grp["tiles"].upd_dtype == torch.float32 for grp in o_g._groups)
-    rep = [(tuple(a.shape), int((a != b).sum()), a.numel(), float((a.float() - b.float()).abs().max()))
+    rep = [(tuple(a.shape), int((a != b).sum()), a.numel(), float((a.detach().float() - b.detach().float()).abs().max()))
            for a, b in zip(p_e, p_g)]
     for a, b in zip(p_e, p_g):
         assert a.dtype == torch.float16
