@@ -85,6 +85,30 @@ def test_ns_untile_equals_ns_then_untile(gdt, pdt, steps, round_once):
         assert bool((b != p0).any()), f"param {i} was not updated"
 
 
+@pytest.mark.parametrize("gdt,pdt", [(F32, BF16), (F32, F32)], ids=["f32-bf16", "f32-f32"])
+def test_ns_untile_many_edge_tiles(gdt, pdt):
+    """Enough tiles that every workgroup runs several work items, most of them
+    on tiles with ragged edges: items whose 32-row blocks go element by
+    element (some issuing no memory operation at all) are followed by further
+    items whose A panel was loaded during their epilogue."""
+    print(f"[ns untile, many edge tiles] {gdt} {pdt}", flush=True)
+    shapes = [(700, 900), (1000, 600), (520, 1030), (600, 1000)] * 16
+    ((p_sep, g_sep), (p_fus, g_fus)), p0s = _pair(shapes, gdt, pdt, False, seed=11)
+    assert g_fus.n_tiles >= 256
+    sa = _groups_table()
+    n = g_sep.n_tiles
+    ws = torch.empty(nat.ns5_workspace_bytes(n, 512, 512), device=DEV, dtype=torch.uint8)
+    g_sep.gather()
+    g_sep.ns(0, n, 5, ws, n)
+    g_sep.untile(5, sa)
+    g_fus.gather()
+    g_fus.ns_untile(0, n, 5, ws, n, sa)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(p_sep, p_fus)):
+        nd = int((a != b).sum())
+        assert nd == 0, f"param {i} {tuple(a.shape)}: {nd} elements differ"
+
+
 def test_ns_untile_falls_back_where_it_does_not_apply():
     """Geometries the fused path does not take are refused before any launch
     (the optimizer then runs NS and the untile as two launches)."""
