@@ -16,7 +16,8 @@
 // Operand stream. K advances in units of 32. Each unit of P (and Q) goes
 // straight from global memory into a 32 KiB slot of a 5-slot LDS ring
 // (global_load_lds_dwordx4, 1 KiB per wave instruction); loads run 4 units
-// ahead of the MFMAs, so up to 128 KiB per CU are in flight. The epilogue
+// ahead of the MFMAs, so up to 128 KiB per CU are in flight (GramA: 4 slots,
+// 3 units ahead). The epilogue
 // operand R (A for GramB, X for Apply) is streamed behind the last K unit as
 // four more 32 KiB units (64 rows x 256 columns each), so it lands while the
 // last MFMAs run. A direct load writes lane l's 16 bytes at 16 l of the wave's
@@ -44,12 +45,15 @@ typedef __attribute__((address_space(3))) u32x4_t lds_u32x4;
 constexpr int BT = 256;               // output block edge
 constexpr int BK = 32;                // K per stream unit
 constexpr int SLOT = 32768;           // bytes per ring slot
-constexpr int NSLOT = 5;              // ring slots
-constexpr int DIST = NSLOT - 1;       // units in flight ahead of the MFMAs
-constexpr int LDS_BYTES = NSLOT * SLOT;
 constexpr int HALF = SLOT / 2;        // Q panel offset within a slot
 
 enum { kGramA = 0, kGramB = 1, kApply = 2 };
+
+// Ring slots; units in flight ahead of the MFMAs = slots - 1. GramB and
+// Apply stream their epilogue operand R as four units behind the K loop
+// and take 5 slots; GramA has no R, and 4 slots are 1-3 % faster there.
+template <int MODE>
+constexpr int kSlots = MODE == kGramA ? 4 : 5;
 
 struct StArgs {
   const uint16_t* P; int64_t p_bs; int ldp;    // rows i (output rows), k-contiguous
@@ -74,32 +78,34 @@ HM_DEV int swz_p(int r) { return (((r >> 1) ^ (r >> 3)) & 1) | (((r >> 2) & 1) <
 HM_DEV int swz_x(int r) { return 10 * (r & 1) + 4 * ((r >> 1) & 1); }
 HM_DEV int swz_c(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
-// vmcnt while waiting for unit w: the loads of the (up to DIST - 1) units
-// issued after it (a K unit is L loads per wave, an R unit RL) and, when this
-// item's first DIST units were prefetched during the previous item's
-// epilogue, the sp global stores of that epilogue, which were issued after
-// unit DIST - 1 and before unit DIST (vmcnt counts loads and stores together
-// and retires them in issue order). sp is 0, 16, 32 or 64; with 64 the count
-// is capped at the counter's maximum, which waits for slightly more than
-// needed.
-template <int L, int NR, int RL>
+// vmcnt while waiting for unit w, with DI units in flight: the loads of the
+// (up to DI - 1) units issued after it (a K unit is L loads per wave, an R
+// unit RL; with rem K units left after w, the rest of the DI - 1 are R units,
+// at most NR) and, when this item's first DI units were prefetched during the
+// previous item's epilogue, the sp global stores of that epilogue, which were
+// issued after unit DI - 1 and before unit DI (vmcnt counts loads and stores
+// together and retires them in issue order). sp is 0, 16, 32 or 64; with 64
+// the count is capped at the counter's maximum, which waits for slightly more
+// than needed.
+template <int L, int NR, int RL, int DI>
 HM_DEV void wait_unit(int nk, int w, int sp) {
+  constexpr auto rmin = [](int a, int b) { return a < b ? a : b; };
   const int rem = nk - 1 - w;
-  if (w < DIST && sp > 0) {  // nk >= 8, so rem >= 4 here; sp is 16, 32 or 64
+  if (w < DI && sp > 0) {  // nk >= 8, so rem >= DI here; sp is 16, 32 or 64
     if (sp > 32)
       wait_vm<63>();
     else if (sp == 16)
-      wait_vm<3 * L + 16>();
+      wait_vm<(DI - 1) * L + 16>();
     else
-      wait_vm<3 * L + 32>();
-  } else if (rem >= 3) {
-    wait_vm<3 * L>();
+      wait_vm<(DI - 1) * L + 32>();
+  } else if (rem >= DI - 1) {
+    wait_vm<(DI - 1) * L>();
   } else if (rem == 2) {
-    wait_vm<2 * L + (NR >= 1 ? RL : 0)>();
+    wait_vm<2 * L + RL * rmin(NR, DI - 3)>();
   } else if (rem == 1) {
-    wait_vm<L + (NR >= 2 ? 2 * RL : RL * NR)>();
+    wait_vm<L + RL * rmin(NR, DI - 2)>();
   } else {
-    wait_vm<(NR >= 3 ? 3 * RL : RL * NR)>();
+    wait_vm<RL * rmin(NR, DI - 1)>();
   }
 }
 
@@ -189,6 +195,8 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
   constexpr int TJ = WC / 32;                     // MFMA tiles along a wave's columns
   constexpr int L = (DIAG ? 16 : 32) / NW;        // K-unit loads per wave
   constexpr int RL = 32 / NW;                     // R-unit loads per wave
+  constexpr int NSLOT = kSlots<MODE>;             // ring slots
+  constexpr int DIST = NSLOT - 1;                 // units in flight ahead of the MFMAs
   const int64_t tile = it.tile;
   const int bi = it.bi, bj = it.bj;
   // The lane index is made opaque per block so that the per-lane addresses
@@ -336,7 +344,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
 #pragma unroll
     for (int v = 0; v < DIST; ++v) issue(v);
   }
-  wait_unit<L, NR, RL>(nk, 0, pre_st);
+  wait_unit<L, NR, RL, DIST>(nk, 0, pre_st);
   scale_unit(0);
   lds_barrier();  // unit 0 is in; every wave is past the previous epilogue's staging
   issue(DIST);
@@ -359,7 +367,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm<0>();  // second-half fragments of unit u
     scale_frags(fa1, fb1);
-    wait_unit<L, NR, RL>(nk, u + 1, pre_st);
+    wait_unit<L, NR, RL, DIST>(nk, u + 1, pre_st);
     scale_unit(u + 1);
     lds_barrier();
     mma_row(fa1, fb1, 0);
@@ -524,7 +532,7 @@ __device__ __forceinline__ int st_item(const StArgs& g, lds_u8* lds, const ItemP
 // 0: K from the arguments). NW: waves per workgroup (4 or 8).
 template <int MODE, int NKC, int NW, bool SC>
 __global__ __launch_bounds__(64 * NW, 1) void ns_st_kernel(StArgs g) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots<MODE> * SLOT];
   const int nbi = g.M / BT, nbj = g.N / BT;
   const int per_tile = (MODE == kApply) ? nbi * nbj : nbi * (nbi + 1) / 2;
   const int64_t total = g.ntiles * per_tile;
