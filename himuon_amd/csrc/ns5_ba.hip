@@ -52,9 +52,12 @@
 //
 //  K loops: the streamed rows go from global memory into a four-unit register
 //  ring (a unit = 32 rows x 64 columns = two k-steps of 16, 4 x 16-byte loads
-//  per lane), three units ahead of the MFMAs; each k-step's 16 rows are
-//  written to one of two wave-private 2 KiB staging buffers and read back as
-//  column fragments with ds_read_b64_tr_b16 (contraction along the rows).
+//  per lane); each k-step's 16 rows are written to one of two wave-private
+//  2 KiB staging buffers one unit before its MFMAs and read back as column
+//  fragments with ds_read_b64_tr_b16 (contraction along the rows). A slot is
+//  free once its rows are staged, so it takes the unit four ahead while the
+//  staged unit's MFMAs run: loads are issued three units before the rows are
+//  staged.
 //  After stage 2 the ring carries the X_P rows i0 .. i0 + 127 (the a X term).
 //
 //  Stage-2 epilogue, per 32-row block: bf16(B X) through the wave's 4 KiB
@@ -88,7 +91,9 @@ constexpr int NKS = T / 16;                 // k-steps per stage
 constexpr int NUNIT = T / 32;               // ring units per stage (2 k-steps each)
 constexpr int HUNIT = NUNIT / 2;            // ring units per K-loop half
 constexpr int NSLOT = 4;                    // ring slots
-constexpr int AHEAD = NSLOT - 1;            // units in flight ahead of the MFMAs
+// units in flight: a unit's rows are staged one unit before its MFMAs, so
+// its slot takes the unit NSLOT ahead while those MFMAs run
+constexpr int AHEAD = NSLOT;
 static_assert(LDS_BYTES == 160 * 1024, "LDS budget");
 
 struct BaArgs {
@@ -325,7 +330,7 @@ HM_DEV int r_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // VMEM instructions a stage-2 epilogue issues after its direct-to-LDS loads
 // (at its second 32-row block) when another item follows: 3 x 4 row stores
-// and 2 x 4 ring loads. The wait for those loads allows this many younger
+// and 3 x 4 ring loads (blocks 1-3). The wait for those loads allows this many younger
 // ones outstanding (vmcnt retires in issue order).
 constexpr int E2_VMEM_AFTER_DMA = 3 * 4 + (AHEAD - 1) * 4;
 static_assert(E2_VMEM_AFTER_DMA < 64, "vmcnt range");
@@ -461,23 +466,19 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     // k-step ks: its 16 rows (ring unit ks / 2, registers 2 (ks % 2) ..) go to
     // staging buffer ks % 2 and come back as column fragments through
     // transposing reads; the row fragments of the panel (A_P or B_P) come from
-    // R. After the first MFMA row of k-step ks, all of k-step ks + 1's reads
-    // (within the half); after the second, k-step ks + 2's rows into buffer
-    // ks % 2, behind those reads (a wave's LDS operations execute in order);
-    // after each row, one load of the unit three ahead.
-    u32x4_t fa[2][2], fb[2][4];
-    auto read_frags = [&](int ks, int b) {
-      const lds_u8* const rb = rfrag_base(ks);
-#pragma unroll
-      for (int ti = 0; ti < 4; ++ti) fb[b][ti] = *reinterpret_cast<const lds_u32x4*>(rb + 32768 * ti);
-      const int buf = 2048 * (ks & 1);
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-        const lds_u8* p = xr0 + buf + ((t2 ^ tr_s) << 6);
-        const u32x2_t lo = read_tr(p);
-        const u32x2_t up = read_tr(p + 512);
-        fa[b][t2] = u32x4_t{lo[0], lo[1], up[0], up[1]};
-      }
+    // R. One register set per fragment, refilled for k-step ks + 1 (within the
+    // half) right after its last MFMA of k-step ks: the column fragment of
+    // row 0 after that row, each row fragment after its MFMA in row 1, the
+    // column fragment of row 1 after it; then k-step ks + 2's rows into
+    // buffer ks % 2, behind those reads (a wave's LDS operations execute in
+    // order). After each row, one load of the unit four ahead (into the slot
+    // of unit u, whose rows were staged during unit u - 1).
+    u32x4_t fa[2], fb[4];
+    auto read_fa = [&](int ks, int t2) {
+      const lds_u8* p = xr0 + 2048 * (ks & 1) + ((t2 ^ tr_s) << 6);
+      const u32x2_t lo = read_tr(p);
+      const u32x2_t up = read_tr(p + 512);
+      fa[t2] = u32x4_t{lo[0], lo[1], up[0], up[1]};
     };
     auto write_rows = [&](int ks, const Unit& su, bool xrows) {
 #pragma unroll
@@ -496,11 +497,22 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     // base: stream index of the stage's unit 0 (0 or 16); hf: the half
     auto khalf = [&](int base, int hf) {
       const bool xrows = base == NUNIT;
+      // stage 2's unit 3 is loaded here rather than in stage 1's last unit,
+      // so that the stage-1 epilogue (all accumulators live) holds three
+      // units in flight, not four
+      if (xrows && hf == 0) load_rows(Xt, 32 * (AHEAD - 1), ring[(NUNIT + AHEAD - 1) % NSLOT]);
       if (hf == 0) {
         write_rows(0, ring[base % NSLOT], xrows);
         write_rows(1, ring[base % NSLOT], xrows);
       }
-      read_frags(2 * HUNIT * hf, 0);
+      {
+        const int ks0 = 2 * HUNIT * hf;
+        const lds_u8* const rb = rfrag_base(ks0);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) fb[ti] = *reinterpret_cast<const lds_u32x4*>(rb + 32768 * ti);
+        read_fa(ks0, 0);
+        read_fa(ks0, 1);
+      }
 #pragma unroll
       for (int uu = 0; uu < HUNIT; ++uu) {
         const int u = HUNIT * hf + uu;
@@ -508,28 +520,28 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
         int row0;
         unit_src(base + u + AHEAD, M, row0);
         Unit& dst = ring[(base + u + AHEAD) % NSLOT];
+        const bool ld = xrows || u + AHEAD < NUNIT + AHEAD - 1;  // stage 2's unit 3: above
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
           const int ks = 2 * u + s;
-          const int b = (s + 1) & 1;
+          const bool nx = ks + 1 < 2 * HUNIT * (hf + 1);  // k-step ks + 1 in this half
 #pragma unroll
-          for (int ti = 0; ti < 4; ++ti) acc[0][ti] = mfma(fa[s][0], fb[s][ti], acc[0][ti]);
+          for (int ti = 0; ti < 4; ++ti) acc[0][ti] = mfma(fa[0], fb[ti], acc[0][ti]);
           __builtin_amdgcn_sched_barrier(0);
-          if (ks + 1 < 2 * HUNIT * (hf + 1)) read_frags(ks + 1, b);
-          load_row(M, row0, dst, 2 * s);
+          if (nx) read_fa(ks + 1, 0);
+          if (ld) load_row(M, row0, dst, 2 * s);
+          const lds_u8* const rb = nx ? rfrag_base(ks + 1) : lds;
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int ti = 0; ti < 4; ++ti) acc[1][ti] = mfma(fa[s][1], fb[s][ti], acc[1][ti]);
-          __builtin_amdgcn_sched_barrier(0);
-          if (ks + 2 < NKS) write_rows(ks + 2, ring[(base + u + 1) % NSLOT], xrows);
-          load_row(M, row0, dst, 2 * s + 1);
-          // Stage 2, last unit: the fourth X_P unit (rows i0 + 96 ..) into
-          // the slot stage-2 unit 15 left (staged during unit 14)
-          if (xrows && u == NUNIT - 1) {
-            Unit& x3 = ring[(2 * NUNIT + AHEAD) % NSLOT];
-            load_row(Xt, i0 + 96, x3, 2 * s);
-            load_row(Xt, i0 + 96, x3, 2 * s + 1);
+          for (int ti = 0; ti < 4; ++ti) {
+            acc[1][ti] = mfma(fa[1], fb[ti], acc[1][ti]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (nx) fb[ti] = *reinterpret_cast<const lds_u32x4*>(rb + 32768 * ti);
+            __builtin_amdgcn_sched_barrier(0);
           }
+          if (nx) read_fa(ks + 1, 1);
+          if (ks + 2 < NKS) write_rows(ks + 2, ring[(base + u + 1) % NSLOT], xrows);
+          if (ld) load_row(M, row0, dst, 2 * s + 1);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -678,8 +690,9 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
 #pragma unroll
         for (int n = 0; n < 4; ++n) gstore16(Yt + (i0 + 32 * ti + 8 * n) * T, xl_o, rows[n]);
       }
-      // the next item's stage-1 units 0..2 into the slots X_P units 0..2 freed
-      if (more && ti < AHEAD) load_rows(nAt, 32 * ti, ring[ti]);
+      // the next item's stage-1 unit ti into the slot X_P unit ti freed
+      static_assert(AHEAD == 4, "one next-item unit per epilogue block");
+      if (more) load_rows(nAt, 32 * ti, ring[ti]);
     }
     if (!more) break;
     // this group's half of the next A_P landed (issued before the
