@@ -548,9 +548,13 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     };
 
     // ---- stage 1: c A_P A^T -----------------------------------------------------------
+    // K loops at a raised wave priority: where one group's K loop meets the
+    // other group's epilogue on a SIMD, the MFMA stream issues first
+    __builtin_amdgcn_s_setprio(1);
     khalf(0, 0);
     lds_barrier();
     khalf(0, 1);
+    __builtin_amdgcn_s_setprio(0);
     lds_barrier();
 
     // ---- stage-1 epilogue: B_P = bf16(c acc + b A_P) over A_P, own columns ----------
@@ -592,9 +596,11 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
         for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
 
     // ---- stage 2: B_P X ---------------------------------------------------------------
+    __builtin_amdgcn_s_setprio(1);
     khalf(NUNIT, 0);
     lds_barrier();
     khalf(NUNIT, 1);
+    __builtin_amdgcn_s_setprio(0);
     lds_barrier();
 
     // ---- stage-2 epilogue -------------------------------------------------------------
