@@ -329,10 +329,14 @@ struct Unit {
 HM_DEV int r_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // VMEM instructions a stage-2 epilogue issues after its direct-to-LDS loads
-// (at its second 32-row block) when another item follows: 3 x 4 row stores
-// and 3 x 4 ring loads (blocks 1-3). The wait for those loads allows this many younger
-// ones outstanding (vmcnt retires in issue order).
-constexpr int E2_VMEM_AFTER_DMA = 3 * 4 + (AHEAD - 1) * 4;
+// (at its third 32-row block) when another item follows: 2 x 4 row stores
+// and 2 x 4 ring loads (blocks 2, 3). The wait for those loads allows this
+// many younger ones outstanding (vmcnt retires in issue order); the ring
+// loads alone are E2_RING_AFTER_DMA. (Issued at the second block, the loads
+// fetched 9 % more from HBM per launch in the same time: the next panel's
+// lines had more time to leave L2 before the tile's streams passed them.)
+constexpr int E2_RING_AFTER_DMA = 2 * 4;
+constexpr int E2_VMEM_AFTER_DMA = 2 * 4 + E2_RING_AFTER_DMA;
 static_assert(E2_VMEM_AFTER_DMA < 64, "vmcnt range");
 
 // SC (the first iteration): every X value (stage-2 rows, the a X term) is
@@ -608,18 +612,18 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     // in the row layout of the stores (row 8 n + l / 8, columns 8 (l % 8) ..).
     const int el32 = lane_o & 31, ehi = lane_o >> 5, erow = lane_o >> 3, ech = lane_o & 7;
     UParam up;
-    bool ufast = true;  // fused untile: blocks 1-3 all took the whole-vector path
+    bool ufast = true;  // fused untile: blocks 2-3 both took the whole-vector path
     if constexpr (UDT >= 0) up = uparam_get(urec, usa);
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
-      if (ti == 1 && more) {
+      if (ti == 2 && more) {
         // The next item's A_P half grp into R (its last readers, the K2
         // halves of both groups over these block columns, are behind
-        // barriers). Every X_P unit is waited for first (only block 0's 4
-        // stores and 4 ring loads may stay in flight), with the compiler's
+        // barriers). Every X_P unit is waited for first (only blocks 0-1's
+        // 8 stores and 8 ring loads may stay in flight), with the compiler's
         // own wait count, so that no wait for an X_P unit follows these
         // loads: it would also wait for them (vmcnt retires in order).
-        wait_vm<8>();
+        wait_vm<16>();
         dma_half(nAt, ni0, grp, lane_o, cw_o);
       }
       const Unit& xp = ring[(2 * NUNIT + ti) % NSLOT];
@@ -689,7 +693,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
           f = ba_untile_block<UDT, false>(up, g.u, make_rows, i0 + 32 * ti + erow, col0 + 8 * ech);
         else
           f = ba_untile_block<UDT, true>(up, g.u, make_rows, i0 + 32 * ti + erow, col0 + 8 * ech);
-        if (ti >= 1) ufast = ufast && f;
+        if (ti >= 2) ufast = ufast && f;
       } else {
         u32x4_t rows[4];
         make_rows(rows);
@@ -709,7 +713,7 @@ __global__ __launch_bounds__(NTH, 1) void ns_ba_kernel(BaArgs g) {
     if (UDT < 0 || ufast)
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(E2_VMEM_AFTER_DMA) : "memory");
     else
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"((AHEAD - 1) * 4) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(E2_RING_AFTER_DMA) : "memory");
     lds_barrier();
     item = next;
   }
